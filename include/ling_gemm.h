@@ -1,0 +1,123 @@
+/*
+ * ling_gemm.h: the C ABI of the MI355X (gfx950) fused quantized GEMM library, libling_gemm.so.
+ *
+ * It is the drop-in for ling-engine's `ling::kernels` quantized GEMM path (reference src/core/kernels.cuh).
+ * Every pointer is caller-owned device memory unless stated; every call is asynchronous on `stream` (a
+ * hipStream_t, NULL = the default stream) and never synchronizes the host. Calls return LQ_OK (0) or an
+ * error code; lq_last_error() then holds the message (per host thread). include/ling_gemm.hpp rethrows
+ * these as std::runtime_error with the reference's message texts.
+ *
+ * Weights are read in the reference's tiled ("kernel-order") layout, byte for byte (reference
+ * src/core/stream_gemm.cu:39-46,705-780): a (16-row tile, 128-value chunk) block is contiguous, blocks in
+ * (tile, chunk) order; FP8 blocks are 2048 bytes, NVFP4 blocks 1024 value bytes + 128 E4M3 scale bytes.
+ *
+ * Activations: BF16 [M][K] (row-major, 16-bit patterns) for the BF16 entry points; FP16 [M][K] with a
+ * power-of-two row scale xinv[M] (to_half_rows) for the reference-compatible ones.
+ *
+ * Scratch: the skinny GEMMs split K across workgroups and reduce the partial sums in a fixed order inside
+ * the kernel; the partials and arrival counters live in a per-device workspace the library allocates on
+ * first use (lq_init allocates it up front so that later calls can be graph-captured). Calls that overlap
+ * on one device (two streams) must not share it: serialize them.
+ */
+#ifndef LING_GEMM_H
+#define LING_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  LQ_OK = 0,
+  LQ_ERR_SHAPE = 1,  /* a shape the kernels do not take (K % 128, N % 16, M out of range, ...) */
+  LQ_ERR_ARG = 2,    /* a null pointer or an invalid argument */
+  LQ_ERR_LAUNCH = 3, /* the HIP runtime reported an error at launch */
+  LQ_ERR_DEVICE = 4  /* device query or workspace allocation failed */
+};
+
+/* Largest row count of the skinny (stream) GEMMs: 5 groups of 16 (4 sequences x 17 verify rows = 68 fit).
+ * The reference takes 32 (kernels.cuh:107, kMaxStreamRows). */
+#define LQ_MAX_STREAM_ROWS 80
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* lq_last_error(void);
+/* Allocates the current device's workspace now (otherwise on first use). No reference counterpart. */
+int lq_init(void);
+/* Library version string. */
+const char* lq_version(void);
+
+/* ---------------- tiled layout (reference src/core/kernels.cuh:162-188) ---------------- */
+size_t lq_tiled_bytes_fp8(int N, int K);          /* kernels.cuh:167 tiled_bytes_fp8 */
+size_t lq_tiled_bytes_nvfp4(int N, int K);        /* kernels.cuh:166 tiled_bytes_nvfp4 */
+size_t lq_tiled_bytes_nvfp4_coded(int N, int K);  /* kernels.cuh:182 tiled_bytes_nvfp4_coded */
+/* Row-major FP8 [N][K] -> tiled. kernels.cuh:169 retile_fp8 */
+int lq_retile_fp8(const uint8_t* w, uint8_t* out, int N, int K, void* stream);
+/* Row-major NVFP4 values [N][K/2] + E4M3 scales [N][K/16] -> tiled. kernels.cuh:168 retile_nvfp4 */
+int lq_retile_nvfp4(const uint8_t* w, const uint8_t* wscale, uint8_t* out, int N, int K, void* stream);
+/* Host: the 6-bit scale-code table (0: more than 64 distinct scales). kernels.cuh:181 scale_code_table */
+int lq_scale_code_table(const uint8_t* scales, size_t n, uint8_t* table64, uint8_t* code_of256);
+/* The coded NVFP4 blob plus a raw scale copy (128 B per block). code_of_dev: device [256].
+ * kernels.cuh:183-184 retile_nvfp4_coded */
+int lq_retile_nvfp4_coded(const uint8_t* w, const uint8_t* wscale, const uint8_t* code_of_dev, uint8_t* out,
+                          uint8_t* raw_scales, int N, int K, void* stream);
+/* Tiled -> BF16 row-major [N][K]: bf16(e4m3 * wscale). kernels.cuh:188 dequant_tiled_fp8 */
+int lq_dequant_tiled_fp8(const uint8_t* tw, float wscale, uint16_t* out, int N, int K, void* stream);
+/* Tiled -> BF16: bf16(e2m1 * (e4m3 * scale2)); raw_scales: a coded blob's raw copy, or NULL.
+ * kernels.cuh:186-187 dequant_tiled_nvfp4 */
+int lq_dequant_tiled_nvfp4(const uint8_t* tw, float scale2, uint16_t* out, int N, int K, void* stream,
+                           const uint8_t* raw_scales);
+/* Additive: tiled FP8 -> FP32 with per-channel scales, e4m3 * wscale_n[n] (the bit-exact dequant check). */
+int lq_dequant_tiled_fp8_pc_f32(const uint8_t* tw, const float* wscale_n, float* out, int N, int K, void* stream);
+/* Additive: tiled NVFP4 -> FP32, e2m1 * (e4m3 * scale2). */
+int lq_dequant_tiled_nvfp4_f32(const uint8_t* tw, float scale2, float* out, int N, int K, void* stream,
+                               const uint8_t* raw_scales);
+
+/* ---------------- rows path, reference-compatible (reference src/core/kernels.cuh:266-295) ------------- */
+/* FP32 x [M][K] -> FP16 with a power-of-two row scale (largest magnitude in [2^14, 2^15)); xinv[m] undoes it.
+ * kernels.cuh:270 to_half_rows */
+int lq_to_half_rows(const float* x, int M, int K, uint16_t* xh, float* xinv, void* stream);
+/* The same from BF16 x. kernels.cuh:546-547 bf16_to_half_rows */
+int lq_bf16_to_half_rows(const uint16_t* x, int M, int K, uint16_t* xh, float* xinv, void* stream);
+/* y[M][N] (FP32) = (wscale * xh . W^T) * xinv[m], W tiled FP8. kernels.cuh:276-277 stream_gemm_fp8 */
+int lq_stream_gemm_fp8(const uint16_t* xh, const float* xinv, int M, const uint8_t* w, float wscale, float* y, int N,
+                       int K, void* stream);
+/* y = (scale2 * xh . W^T) * xinv[m], W tiled NVFP4 (table: a coded blob's scale-code table, device [64], or
+ * NULL for a raw blob). kernels.cuh:273-274 stream_gemm_nvfp4 */
+int lq_stream_gemm_nvfp4(const uint16_t* xh, const float* xinv, int M, const uint8_t* w, const uint8_t* table,
+                         float scale2, float* y, int N, int K, void* stream);
+/* kernels.cuh:281-287 StreamTarget */
+typedef struct {
+  const uint8_t* w;
+  const uint8_t* wscale; /* NVFP4: coded blob's table (device), else NULL */
+  float scale;           /* NVFP4 global scale or FP8 per-tensor scale */
+  float* y;
+  int N;
+} lq_stream_target;
+/* 1..4 matrices sharing xh in one launch, each y = scale * xh . W^T * xinv. kernels.cuh:288-289 stream_gemm_multi */
+int lq_stream_gemm_multi(int nvfp4, const uint16_t* xh, const float* xinv, int M, const lq_stream_target* t, int n,
+                         int K, void* stream);
+
+/* ---------------- rows path, BF16 formats (additive; per-channel FP8 scales, BF16 in and out) ---------------- */
+/* y[M][N] = bf16(wscale_n[n] * x . W^T), W tiled FP8, x BF16 [M][K]. Replaces the engine's linear_fp8
+ * (reference src/core/engine.cpp:1272-1281) for per-channel checkpoints. */
+int lq_stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N, int K,
+                     void* stream);
+/* h[M][N] = bf16(silu(sg[n] * x . G^T) * (su[n] * x . U^T)): the MLP gate/up projections with the SiLU*mul
+ * epilogue fused (reference engine.cpp:1699-1701 = stream_gemm_multi({gate, up}) + silu_mul). */
+int lq_stream_fp8_pc_silu_mul(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate,
+                              const uint8_t* w_up, const float* s_up, uint16_t* h, int N, int K, void* stream);
+/* y[M][N] = bf16(wscale_n[n] * x . W^T + resid[m][n]); y may be resid (in place). The down / out projection
+ * with the residual add fused (reference engine.cpp:1227-1233 linear_fp8_residual = stream_gemm + add_inplace). */
+int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n,
+                              const uint16_t* resid, uint16_t* y, int N, int K, void* stream);
+/* y[M][N] = bf16(scale2 * x . W^T), W tiled NVFP4 (raw, or coded with its device table), x BF16: converts x
+ * to the FP16 row copy in the workspace, then streams. Replaces linear_fp4 (engine.cpp:1173-1177). */
+int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
+                         int N, int K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,27 @@
+// Per-device workspace of the skinny GEMMs: split-K partial sums, per-tile-group arrival counters (kept
+// zero between launches: the last workgroup of a group resets its counter), and the FP16 activation copy
+// of the BF16-input NVFP4 entry point. Grow-only; allocated on first use or by lq_init().
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+namespace lq {
+
+struct Workspace {
+  float* partials = nullptr;
+  size_t partial_bytes = 0;
+  int* counters = nullptr;
+  size_t counter_count = 0;
+  uint16_t* xh = nullptr;
+  float* xinv = nullptr;
+  size_t half_elems = 0;
+  // Ensure capacity; returns LQ_OK or LQ_ERR_DEVICE (message set).
+  int reserve_stream(size_t partial_bytes_needed, size_t counters_needed);
+  int reserve_half(size_t elems);
+};
+
+// The calling thread's current device's workspace (created on first call), or null (error set).
+Workspace* workspace_for_current_device();
+
+}  // namespace lq

@@ -1,0 +1,266 @@
+"""Python binding of libling_gemm.so (the C ABI in include/ling_gemm.h) over torch device tensors.
+
+torch provides device memory and the stream (plumbing); every computation runs in the library's HIP
+kernels. The module fails loudly when the library is missing: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libling_gemm.so")
+
+MAX_STREAM_ROWS = 80
+
+# exported symbols and signatures (argument order of include/ling_gemm.h)
+_P, _I, _F, _SZ = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+SIGNATURES = {
+    "lq_last_error": (C.c_char_p, []),
+    "lq_init": (_I, []),
+    "lq_version": (C.c_char_p, []),
+    "lq_tiled_bytes_fp8": (_SZ, [_I, _I]),
+    "lq_tiled_bytes_nvfp4": (_SZ, [_I, _I]),
+    "lq_tiled_bytes_nvfp4_coded": (_SZ, [_I, _I]),
+    "lq_retile_fp8": (_I, [_P, _P, _I, _I, _P]),
+    "lq_retile_nvfp4": (_I, [_P, _P, _P, _I, _I, _P]),
+    "lq_scale_code_table": (_I, [_P, _SZ, _P, _P]),
+    "lq_retile_nvfp4_coded": (_I, [_P, _P, _P, _P, _P, _I, _I, _P]),
+    "lq_dequant_tiled_fp8": (_I, [_P, _F, _P, _I, _I, _P]),
+    "lq_dequant_tiled_nvfp4": (_I, [_P, _F, _P, _I, _I, _P, _P]),
+    "lq_dequant_tiled_fp8_pc_f32": (_I, [_P, _P, _P, _I, _I, _P]),
+    "lq_dequant_tiled_nvfp4_f32": (_I, [_P, _F, _P, _I, _I, _P, _P]),
+    "lq_to_half_rows": (_I, [_P, _I, _I, _P, _P, _P]),
+    "lq_bf16_to_half_rows": (_I, [_P, _I, _I, _P, _P, _P]),
+    "lq_stream_gemm_fp8": (_I, [_P, _P, _I, _P, _F, _P, _I, _I, _P]),
+    "lq_stream_gemm_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _I, _I, _P]),
+    "lq_stream_gemm_multi": (_I, [_I, _P, _P, _I, _P, _I, _I, _P]),
+    "lq_stream_fp8_pc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_fp8_pc_residual": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
+}
+
+
+class StreamTarget(C.Structure):
+    _fields_ = [("w", C.c_void_p), ("wscale", C.c_void_p), ("scale", C.c_float), ("y", C.c_void_p), ("N", C.c_int)]
+
+
+class LingGemmError(RuntimeError):
+    pass
+
+
+def load_library(path: str = LIB_PATH) -> C.CDLL:
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                          "(or make -C ling-engine_amd/csrc)")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = load_library()
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise LingGemmError(lib.lq_last_error().decode())
+
+
+def _dev(t: torch.Tensor, dtype=None) -> torch.Tensor:
+    if not t.is_cuda:
+        raise ValueError("expected a device tensor")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"expected {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError("expected a contiguous tensor")
+    return t
+
+
+def init() -> None:
+    _check(lib.lq_init())
+
+
+# ---------------- layout ----------------
+def tiled_bytes_fp8(N: int, K: int) -> int:
+    return lib.lq_tiled_bytes_fp8(N, K)
+
+
+def tiled_bytes_nvfp4(N: int, K: int) -> int:
+    return lib.lq_tiled_bytes_nvfp4(N, K)
+
+
+def tiled_bytes_nvfp4_coded(N: int, K: int) -> int:
+    return lib.lq_tiled_bytes_nvfp4_coded(N, K)
+
+
+def retile_fp8(w: torch.Tensor) -> torch.Tensor:
+    """Row-major FP8 codes [N][K] (uint8) -> the tiled blob (uint8)."""
+    N, K = w.shape
+    out = torch.empty(tiled_bytes_fp8(N, K), dtype=torch.uint8, device=w.device)
+    _check(lib.lq_retile_fp8(_ptr(_dev(w, torch.uint8)), _ptr(out), N, K, _stream()))
+    return out
+
+
+def retile_nvfp4(values: torch.Tensor, scales: torch.Tensor) -> torch.Tensor:
+    N = values.shape[0]
+    K = values.shape[1] * 2
+    out = torch.empty(tiled_bytes_nvfp4(N, K), dtype=torch.uint8, device=values.device)
+    _check(lib.lq_retile_nvfp4(_ptr(_dev(values, torch.uint8)), _ptr(_dev(scales, torch.uint8)), _ptr(out), N, K,
+                               _stream()))
+    return out
+
+
+def scale_code_table(scales_host) -> tuple[bool, bytes, bytes]:
+    import numpy as np
+    s = np.ascontiguousarray(scales_host, dtype=np.uint8).reshape(-1)
+    table = np.zeros(64, np.uint8)
+    code_of = np.zeros(256, np.uint8)
+    ok = lib.lq_scale_code_table(s.ctypes.data_as(C.c_void_p), s.size, table.ctypes.data_as(C.c_void_p),
+                                 code_of.ctypes.data_as(C.c_void_p))
+    return bool(ok), table, code_of
+
+
+def retile_nvfp4_coded(values: torch.Tensor, scales: torch.Tensor, code_of: torch.Tensor):
+    N = values.shape[0]
+    K = values.shape[1] * 2
+    out = torch.empty(tiled_bytes_nvfp4_coded(N, K), dtype=torch.uint8, device=values.device)
+    raw = torch.empty(N * K // 16, dtype=torch.uint8, device=values.device)
+    _check(lib.lq_retile_nvfp4_coded(_ptr(_dev(values, torch.uint8)), _ptr(_dev(scales, torch.uint8)),
+                                     _ptr(_dev(code_of, torch.uint8)), _ptr(out), _ptr(raw), N, K, _stream()))
+    return out, raw
+
+
+def dequant_tiled_fp8(tw: torch.Tensor, wscale: float, N: int, K: int) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=tw.device)
+    _check(lib.lq_dequant_tiled_fp8(_ptr(tw), wscale, _ptr(out), N, K, _stream()))
+    return out
+
+
+def dequant_tiled_fp8_pc_f32(tw: torch.Tensor, wscale_n: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=torch.float32, device=tw.device)
+    _check(lib.lq_dequant_tiled_fp8_pc_f32(_ptr(tw), _ptr(_dev(wscale_n, torch.float32)), _ptr(out), N, K, _stream()))
+    return out
+
+
+def dequant_tiled_nvfp4(tw: torch.Tensor, scale2: float, N: int, K: int, raw_scales=None) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=tw.device)
+    _check(lib.lq_dequant_tiled_nvfp4(_ptr(tw), scale2, _ptr(out), N, K, _stream(), _ptr(raw_scales)))
+    return out
+
+
+def dequant_tiled_nvfp4_f32(tw: torch.Tensor, scale2: float, N: int, K: int, raw_scales=None) -> torch.Tensor:
+    out = torch.empty((N, K), dtype=torch.float32, device=tw.device)
+    _check(lib.lq_dequant_tiled_nvfp4_f32(_ptr(tw), scale2, _ptr(out), N, K, _stream(), _ptr(raw_scales)))
+    return out
+
+
+# ---------------- rows path, reference-compatible ----------------
+def to_half_rows(x: torch.Tensor):
+    M, K = x.shape
+    xh = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    xinv = torch.empty(M, dtype=torch.float32, device=x.device)
+    _check(lib.lq_to_half_rows(_ptr(_dev(x, torch.float32)), M, K, _ptr(xh), _ptr(xinv), _stream()))
+    return xh, xinv
+
+
+def bf16_to_half_rows(x: torch.Tensor):
+    M, K = x.shape
+    xh = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    xinv = torch.empty(M, dtype=torch.float32, device=x.device)
+    _check(lib.lq_bf16_to_half_rows(_ptr(_dev(x, torch.bfloat16)), M, K, _ptr(xh), _ptr(xinv), _stream()))
+    return xh, xinv
+
+
+def stream_gemm_fp8(xh, xinv, w, wscale: float, N: int, K: int, y=None):
+    M = xh.shape[0]
+    y = torch.empty((M, N), dtype=torch.float32, device=xh.device) if y is None else y
+    _check(lib.lq_stream_gemm_fp8(_ptr(_dev(xh, torch.float16)), _ptr(xinv), M, _ptr(w), wscale, _ptr(y), N, K,
+                                  _stream()))
+    return y
+
+
+def stream_gemm_nvfp4(xh, xinv, w, table, scale2: float, N: int, K: int, y=None):
+    M = xh.shape[0]
+    y = torch.empty((M, N), dtype=torch.float32, device=xh.device) if y is None else y
+    _check(lib.lq_stream_gemm_nvfp4(_ptr(_dev(xh, torch.float16)), _ptr(xinv), M, _ptr(w), _ptr(table), scale2,
+                                    _ptr(y), N, K, _stream()))
+    return y
+
+
+def stream_gemm_multi(nvfp4: bool, xh, xinv, targets, K: int):
+    """targets: list of (w, table_or_None, scale, y, N)."""
+    M = xh.shape[0]
+    arr = (StreamTarget * len(targets))()
+    for i, (w, tab, sc, y, N) in enumerate(targets):
+        arr[i] = StreamTarget(w.data_ptr(), tab.data_ptr() if tab is not None else None, sc, y.data_ptr(), N)
+    _check(lib.lq_stream_gemm_multi(int(nvfp4), _ptr(_dev(xh, torch.float16)), _ptr(xinv), M, arr, len(targets), K,
+                                    _stream()))
+
+
+# ---------------- rows path, BF16 formats ----------------
+def stream_fp8_pc(x, w, wscale_n, N: int, y=None):
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if y is None else y
+    _check(lib.lq_stream_fp8_pc(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(_dev(wscale_n, torch.float32)),
+                                _ptr(y), N, K, _stream()))
+    return y
+
+
+def stream_fp8_pc_silu_mul(x, w_gate, s_gate, w_up, s_up, N: int, h=None):
+    M, K = x.shape
+    h = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if h is None else h
+    _check(lib.lq_stream_fp8_pc_silu_mul(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w_gate), _ptr(s_gate), _ptr(w_up),
+                                         _ptr(s_up), _ptr(h), N, K, _stream()))
+    return h
+
+
+def stream_fp8_pc_residual(x, w, wscale_n, resid, N: int, y=None):
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if y is None else y
+    _check(lib.lq_stream_fp8_pc_residual(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(wscale_n),
+                                         _ptr(_dev(resid, torch.bfloat16)), _ptr(y), N, K, _stream()))
+    return y
+
+
+def stream_nvfp4_bf16(x, w, table, scale2: float, N: int, y=None):
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if y is None else y
+    _check(lib.lq_stream_nvfp4_bf16(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(table), scale2, _ptr(y), N, K,
+                                    _stream()))
+    return y
+
+
+# ---------------- prefill ----------------
+def quant_act_fp8_g128(x):
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((M, K // 128), dtype=torch.float32, device=x.device)
+    _check(lib.lq_quant_act_fp8_g128(_ptr(_dev(x, torch.bfloat16)), M, K, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def prefill_fp8_block(xq, xs, w, ws, N: int, y=None, ldy: int | None = None):
+    M, K = xq.shape
+    ldy = N if ldy is None else ldy
+    y = torch.empty((M, ldy), dtype=torch.bfloat16, device=xq.device) if y is None else y
+    _check(lib.lq_prefill_fp8_block(_ptr(_dev(xq, torch.uint8)), _ptr(_dev(xs, torch.float32)), M, _ptr(w),
+                                    _ptr(_dev(ws, torch.float32)), _ptr(y), ldy, N, K, _stream()))
+    return y

@@ -1,0 +1,66 @@
+"""CPU-side checks of the C ABI library: it loads, exports every entry point include/ling_gemm.h declares, and
+its host-only functions behave (no device work is started here)."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+
+import oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ling_gemm.h")
+LIB = os.path.join(ROOT, "ling-engine_amd", "libling_gemm.so")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(lq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = C.CDLL(LIB)
+    names = declared_functions()
+    assert len(names) >= 20
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_the_header():
+    import ling_gemm
+    assert set(declared_functions()) == set(ling_gemm.SIGNATURES)
+
+
+def test_tiled_sizes_match_oracle():
+    import ling_gemm as L
+    for N, K in [(16, 128), (5120, 5120), (34816, 5120), (5120, 17408), (5120, 25600)]:
+        assert L.tiled_bytes_fp8(N, K) == O.lib.or_tiled_bytes_fp8(N, K)
+        assert L.tiled_bytes_nvfp4(N, K) == O.lib.or_tiled_bytes_nvfp4(N, K)
+        assert L.tiled_bytes_nvfp4_coded(N, K) == O.lib.or_tiled_bytes_nvfp4_coded(N, K)
+
+
+def test_scale_code_table_matches_oracle():
+    import ling_gemm as L
+    w = O.normal_bf16(12, 0.02, (64, 512))
+    _, s, _, _ = O.quant_nvfp4(w)
+    ok, table, code_of = L.scale_code_table(s)
+    ok2, table2, code_of2 = O.scale_code_table(s)
+    assert ok and ok2
+    assert np.array_equal(table, table2) and np.array_equal(code_of, code_of2)
+    assert not L.scale_code_table(np.arange(100, dtype=np.uint8))[0]
+
+
+def test_errors_are_reported_before_any_launch():
+    import ling_gemm as L
+    lib = L.lib
+    # shape errors come back as status codes with the reference's message texts, no device touched
+    assert lib.lq_stream_fp8_pc(None, 1, None, None, None, 16, 100, None) == 1
+    assert b"K must be a multiple of 128" in lib.lq_last_error()
+    assert lib.lq_stream_fp8_pc(None, 1, None, None, None, 16, 128, None) == 2  # then null pointers
+    assert lib.lq_stream_gemm_fp8(None, None, 81, None, 1.0, None, 16, 128, None) == 1
+    assert b"M must be in [1, 80]" in lib.lq_last_error()
+    assert lib.lq_stream_gemm_multi(0, None, None, 1, None, 5, 128, None) == 1
+    assert b"1 to 4 matrices per launch" in lib.lq_last_error()
+    assert lib.lq_retile_fp8(None, None, 17, 128, None) == 1
+    assert b"N % 16 and K % 128 must be 0" in lib.lq_last_error()

@@ -1,0 +1,245 @@
+"""Parity of the skinny (stream) GEMMs on the GPU against the CPU oracle, through the C ABI.
+
+Bounds: on BF16 outputs, max relative error <= 1e-2 and mean |got - ref| <= 1e-3, with the
+relative error of an element |got - ref| / max(|ref|, rms(ref row)) (robust to outputs near zero; one BF16 ulp is
+at most 2^-8 of it),
+where ref is the oracle (dequantize to FP32, FP32 accumulate, one BF16 rounding); dequantized weights and the
+layout are bit-exact. Rows of every M are bit-identical to the same rows of a larger launch (row invariance,
+reference src/core/stream_gemm.cu:10-13, tests/stream_tests.cu:206-224).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module")
+def L():
+    import ling_gemm
+    ling_gemm.init()
+    return ling_gemm
+
+
+def to_dev(a: np.ndarray, dtype=None) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    return t.view(dtype) if dtype is not None else t
+
+
+def bf16_dev(bits: np.ndarray) -> torch.Tensor:
+    return to_dev(bits.view(np.int16)).view(torch.bfloat16)
+
+
+def bf16_host(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def assert_close_bf16(got_bits: np.ndarray, ref_bits: np.ndarray, what: str):
+    got = O.bf16_to_f32(got_bits).astype(np.float64)
+    ref = O.bf16_to_f32(ref_bits).astype(np.float64)
+    assert np.isfinite(got).all(), what
+    rms = np.sqrt(np.mean(ref * ref, axis=-1, keepdims=True)) + 1e-30
+    rel = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms))
+    mae = np.mean(np.abs(got - ref))
+    assert rel <= 1e-2, f"{what}: max rel err {rel:.3e}"
+    assert mae <= 1e-3, f"{what}: mean abs err {mae:.3e}"
+    return rel, mae
+
+
+def fp8_weights(seed, N, K):
+    w = O.normal_f32(seed, 0.02, (N, K))
+    return O.quant_fp8_per_channel(w)
+
+
+# ---------------------------------------------------------------- layout / dequant
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 384), (528, 2048)])
+def test_retile_fp8_bytes_and_dequant_bit_exact(L, N, K):
+    q, s = fp8_weights(1, N, K)
+    tw = L.retile_fp8(to_dev(q))
+    assert np.array_equal(tw.cpu().numpy(), O.retile_fp8(q))
+    got = L.dequant_tiled_fp8_pc_f32(tw, to_dev(s), N, K).cpu().numpy()
+    want = O.dequant_fp8_pc(q, s)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    gb = bf16_host(L.dequant_tiled_fp8(tw, 0.021, N, K))
+    wb = O.f32_to_bf16(O.dequant_fp8_pc(q, np.full(N, 0.021, np.float32)))
+    assert np.array_equal(gb, wb)
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (528, 2048)])
+def test_retile_nvfp4_raw_and_coded_bytes_and_dequant(L, N, K):
+    w = O.normal_bf16(2, 0.02, (N, K))
+    v, s, g, _ = O.quant_nvfp4(w)
+    tw = L.retile_nvfp4(to_dev(v), to_dev(s))
+    assert np.array_equal(tw.cpu().numpy(), O.retile_nvfp4(v, s))
+    got = L.dequant_tiled_nvfp4_f32(tw, g, N, K).cpu().numpy()
+    want = O.dequant_nvfp4(v, s, g)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(bf16_host(L.dequant_tiled_nvfp4(tw, g, N, K)), O.f32_to_bf16(want))
+    ok, table, code_of = O.scale_code_table(s)
+    assert ok
+    blob, raw = L.retile_nvfp4_coded(to_dev(v), to_dev(s), to_dev(code_of))
+    oblob, oraw = O.retile_nvfp4_coded(v, s, code_of)
+    assert np.array_equal(blob.cpu().numpy(), oblob)
+    assert np.array_equal(raw.cpu().numpy(), oraw)
+    got2 = L.dequant_tiled_nvfp4_f32(blob, g, N, K, raw).cpu().numpy()
+    assert np.array_equal(got2.view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- BF16 per-channel FP8 path
+MS = [1, 2, 7, 15, 16, 17, 24, 31, 32, 33, 48, 64, 68, 80]
+
+
+@pytest.mark.parametrize("N,K", [(528, 2048), (16, 128), (1040, 384)])
+def test_stream_fp8_pc_parity_and_row_invariance(L, N, K):
+    q, s = fp8_weights(3, N, K)
+    x = O.normal_bf16(4, 1.0, (80, K))
+    tw = L.retile_fp8(to_dev(q))
+    sd = to_dev(s)
+    xd = bf16_dev(x)
+    ref = O.stream_fp8_pc_bf16(x, q, s)
+    full = bf16_host(L.stream_fp8_pc(xd, tw, sd, N))
+    assert_close_bf16(full, ref, f"M=80 N={N} K={K}")
+    for M in MS:
+        got = bf16_host(L.stream_fp8_pc(xd[:M].contiguous(), tw, sd, N))
+        assert np.array_equal(got, full[:M]), f"row invariance M={M}"
+
+
+def test_stream_fp8_pc_silu_mul(L):
+    N, K = 1024, 1280
+    qg, sg = fp8_weights(5, N, K)
+    qu, su = fp8_weights(6, N, K)
+    x = O.normal_bf16(7, 1.0, (68, K))
+    twg, twu = L.retile_fp8(to_dev(qg)), L.retile_fp8(to_dev(qu))
+    xd = bf16_dev(x)
+    xf = O.bf16_to_f32(x)
+    gacc = O.gemm_f32(xf, O.dequant_fp8_pc(qg, sg))
+    uacc = O.gemm_f32(xf, O.dequant_fp8_pc(qu, su))
+    ref = O.epi_silu_mul_bf16(gacc, uacc)
+    full = bf16_host(L.stream_fp8_pc_silu_mul(xd, twg, to_dev(sg), twu, to_dev(su), N))
+    assert_close_bf16(full, ref, "silu_mul M=68")
+    for M in [1, 17, 33]:
+        got = bf16_host(L.stream_fp8_pc_silu_mul(xd[:M].contiguous(), twg, to_dev(sg), twu, to_dev(su), N))
+        assert np.array_equal(got, full[:M])
+
+
+def test_stream_fp8_pc_residual_in_place(L):
+    N, K = 512, 2048
+    q, s = fp8_weights(8, N, K)
+    x = O.normal_bf16(9, 1.0, (17, K))
+    r = O.normal_bf16(10, 1.0, (17, N))
+    tw = L.retile_fp8(to_dev(q))
+    acc = O.gemm_f32(O.bf16_to_f32(x), O.dequant_fp8_pc(q, s))
+    ref = O.epi_residual_bf16(acc, r)
+    rd = bf16_dev(r)
+    out = bf16_host(L.stream_fp8_pc_residual(bf16_dev(x), tw, to_dev(s), rd, N))
+    assert_close_bf16(out, ref, "residual")
+    L.stream_fp8_pc_residual(bf16_dev(x), tw, to_dev(s), rd, N, y=rd)  # in place
+    assert np.array_equal(bf16_host(rd), out)
+
+
+# ---------------------------------------------------------------- reference-compatible FP16 path
+def reference_rows(x: np.ndarray, wdeq: np.ndarray) -> np.ndarray:
+    return (x.astype(np.float64) @ wdeq.astype(np.float64).T)
+
+
+def test_to_half_rows_bit_exact(L):
+    x = O.normal_f32(11, 1.0, (24, 5120))
+    x[1] = 0
+    x[2, 77] = 3.0e30
+    x[3, 5119] = np.inf
+    xh, xinv = L.to_half_rows(to_dev(x))
+    wh, winv = O.to_half_rows(x)
+    assert np.array_equal(xh.view(torch.int16).cpu().numpy().view(np.uint16), wh)
+    assert np.array_equal(xinv.cpu().numpy(), winv)
+    xb = O.f32_to_bf16(O.normal_f32(12, 1.0, (16, 25600)))
+    bh, binv = L.bf16_to_half_rows(bf16_dev(xb))
+    wh2, winv2 = O.to_half_rows(O.bf16_to_f32(xb))
+    assert np.array_equal(bh.view(torch.int16).cpu().numpy().view(np.uint16), wh2)
+    assert np.array_equal(binv.cpu().numpy(), winv2)
+
+
+def reference_style_weights(seed, N, K):
+    """tests/stream_tests.cu:147-160: random bytes (no E4M3 NaN), NVFP4 scales 0x28..0x48, x with outliers."""
+    rng = np.random.default_rng(seed)
+    w8 = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    w8[(w8 & 0x7F) == 0x7F] = 0x10
+    w4 = rng.integers(0, 256, (N, K // 2), dtype=np.uint8)
+    s4 = rng.integers(0x28, 0x49, (N, K // 16), dtype=np.uint8)
+    x = O.normal_f32(seed + 1, 1.0, (32, K))
+    x.reshape(-1)[::97] *= 30.0
+    return w8, w4, s4, x
+
+
+def test_stream_gemm_fp8_and_nvfp4_reference_compatible(L):
+    N, K = 528, 2048
+    w8, w4, s4, x = reference_style_weights(11, N, K)
+    gs4, gs8 = 0.37, 0.021
+    t8 = L.retile_fp8(to_dev(w8))
+    t4 = L.retile_nvfp4(to_dev(w4), to_dev(s4))
+    xh, xinv = L.to_half_rows(to_dev(x))
+    ref8 = reference_rows(x, O.dequant_fp8_pc(w8, np.full(N, gs8, np.float32)))
+    ref4 = reference_rows(x, O.dequant_nvfp4(w4, s4, gs4))
+    for fp4, ref in [(False, ref8), (True, ref4)]:
+        full = (L.stream_gemm_nvfp4(xh, xinv, t4, None, gs4, N, K) if fp4 else
+                L.stream_gemm_fp8(xh, xinv, t8, gs8, N, K)).cpu().numpy()
+        rms = np.sqrt(np.mean(ref ** 2, axis=1, keepdims=True))
+        # the reference's own bound (tests/stream_tests.cu:211-218)
+        assert np.max(np.abs(full - ref) / rms) < 2e-3
+        for M in [1, 2, 7, 8, 9, 15, 16, 17, 20, 24, 25, 32]:
+            got = (L.stream_gemm_nvfp4(xh[:M].contiguous(), xinv[:M].contiguous(), t4, None, gs4, N, K) if fp4 else
+                   L.stream_gemm_fp8(xh[:M].contiguous(), xinv[:M].contiguous(), t8, gs8, N, K)).cpu().numpy()
+            assert np.array_equal(got, full[:M])
+
+
+def test_coded_equals_raw_and_multi_equals_separate(L):
+    N, K = 528, 1024
+    w = O.normal_bf16(13, 0.02, (N, K))
+    v, s, g, _ = O.quant_nvfp4(w)
+    ok, table, code_of = O.scale_code_table(s)
+    assert ok
+    raw = L.retile_nvfp4(to_dev(v), to_dev(s))
+    blob, _ = L.retile_nvfp4_coded(to_dev(v), to_dev(s), to_dev(code_of))
+    tab = to_dev(table)
+    x = O.normal_f32(14, 1.0, (20, K))
+    xh, xinv = L.to_half_rows(to_dev(x))
+    a = L.stream_gemm_nvfp4(xh, xinv, raw, None, g, N, K).cpu().numpy()
+    b = L.stream_gemm_nvfp4(xh, xinv, blob, tab, g, N, K).cpu().numpy()
+    assert np.array_equal(a, b)
+    q8, _ = fp8_weights(15, 256, K)
+    t8 = L.retile_fp8(to_dev(q8))
+    y8 = L.stream_gemm_fp8(xh, xinv, t8, 0.5, 256, K).cpu().numpy()
+    ya = torch.empty((20, N), dtype=torch.float32, device=DEV)
+    yb = torch.empty((20, N), dtype=torch.float32, device=DEV)
+    L.stream_gemm_multi(True, xh, xinv, [(raw, None, g, ya, N), (blob, tab, g, yb, N)], K)
+    assert np.array_equal(ya.cpu().numpy(), a) and np.array_equal(yb.cpu().numpy(), a)
+    y1 = torch.empty((20, 256), dtype=torch.float32, device=DEV)
+    y2 = torch.empty((20, 256), dtype=torch.float32, device=DEV)
+    L.stream_gemm_multi(False, xh, xinv, [(t8, None, 0.5, y1, 256), (t8, None, 0.5, y2, 256)], K)
+    assert np.array_equal(y1.cpu().numpy(), y8) and np.array_equal(y2.cpu().numpy(), y8)
+
+
+def test_stream_nvfp4_bf16(L):
+    N, K = 512, 2560
+    w = O.normal_bf16(16, 0.02, (N, K))
+    v, s, g, _ = O.quant_nvfp4(w)
+    tw = L.retile_nvfp4(to_dev(v), to_dev(s))
+    x = O.normal_bf16(17, 1.0, (16, K))
+    ref = O.f32_to_bf16(O.gemm_f32(O.bf16_to_f32(x), O.dequant_nvfp4(v, s, g)))
+    got = bf16_host(L.stream_nvfp4_bf16(bf16_dev(x), tw, None, g, N))
+    assert_close_bf16(got, ref, "nvfp4 bf16")
+
+
+def test_error_paths(L):
+    q, s = fp8_weights(1, 16, 128)
+    tw = L.retile_fp8(to_dev(q))
+    x = bf16_dev(O.normal_bf16(1, 1.0, (81, 128)))
+    with pytest.raises(L.LingGemmError, match=r"M must be in \[1, 80\]"):
+        L.stream_fp8_pc(x, tw, to_dev(s), 16)
+    with pytest.raises(L.LingGemmError, match="K must be a multiple of 128"):
+        L.stream_fp8_pc(bf16_dev(O.normal_bf16(1, 1.0, (2, 100))), tw, to_dev(s), 16)
+    with pytest.raises(L.LingGemmError, match="N % 16"):
+        L.stream_fp8_pc(x[:2].contiguous(), tw, to_dev(s), 24)

@@ -1,0 +1,273 @@
+"""Pins the CPU oracle (the checker) before anything is checked against it.
+
+Every codec is compared exhaustively with torch's independent float8_e4m3fn / bfloat16 / float16 casts; the
+NVFP4 weight quantizer with the reference's hand-made block and error band (tests/stream_tests.cu:1093-1119);
+the tiled layout with literal byte positions from the reference's layout description
+(src/core/stream_gemm.cu:15-21,39-46,705-738) and round trips; the GEMM with a float64 product.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+def test_e4m3_decode_all_codes_vs_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = np.array([O.lib.or_e4m3_decode(int(c)) for c in codes], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))  # signed zeros too
+    assert O.lib.or_e4m3_decode(0x7E) == 448.0 and O.lib.or_e4m3_decode(0x01) == 2.0 ** -9
+
+
+def _torch_e4m3_satfinite(x: np.ndarray) -> np.ndarray:
+    t = torch.from_numpy(x).clamp(-448.0, 448.0)
+    return t.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+
+
+def test_e4m3_encode_vs_torch_rne():
+    rng = np.random.default_rng(1)
+    # every midpoint and neighbour of the grid, plus random magnitudes over the whole range and past it
+    grid = np.array([O.lib.or_e4m3_decode(c) for c in range(0x7F)], np.float64)
+    mids = (grid[1:] + grid[:-1]) / 2
+    pts = np.concatenate([grid, mids, np.nextafter(mids, 0), np.nextafter(mids, 1e9),
+                          rng.uniform(0, 500, 20000), np.exp(rng.uniform(-14, 7, 20000)), [0.0, 1e-30, 447.9, 448,
+                                                                                             449, 463, 464, 480, 1e6]])
+    x = np.concatenate([pts, -pts]).astype(np.float32)
+    got = np.array([O.lib.or_e4m3_encode(float(v)) for v in x], np.uint8)
+    assert np.array_equal(got, _torch_e4m3_satfinite(x))
+
+
+def test_bf16_and_f16_vs_torch():
+    rng = np.random.default_rng(2)
+    x = np.concatenate([rng.standard_normal(20000) * 10.0 ** rng.integers(-40, 38, 20000),
+                        [0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e-8, 6e-8, 3e-5, 3.3895e38, 1e-45]]).astype(np.float32)
+    x = x[np.isfinite(x)]
+    want_bf = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got_bf = O.f32_to_bf16(x)
+    assert np.array_equal(got_bf, want_bf)
+    small = x[np.abs(x) < 1e6]
+    want_h = torch.from_numpy(small).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    got_h = np.array([O.lib.or_f16_bits(float(v)) for v in small], np.uint16)
+    assert np.array_equal(got_h, want_h)
+    for h in range(0, 65536, 7):
+        want = torch.tensor([h], dtype=torch.int16 if h < 32768 else torch.int32).to(torch.int16).view(
+            torch.float16).float().item() if h < 32768 else None
+        if want is not None and not np.isnan(want):
+            assert O.lib.or_f16_float(h) == want
+
+
+def test_e2m1_decode_table_literal():
+    # src/core/stream_gemm.cu:782 and tests/stream_tests.cu:34
+    want = [0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6]
+    got = [O.lib.or_e2m1_decode(c) for c in range(16)]
+    assert got == want and np.signbit(got[8])
+
+
+def test_e2m1_activation_rne_ties_even():
+    # halfway points between codes: 0.25->0, 0.75->1.0(code2), 1.25->1.0, 1.75->2.0, 2.5->2.0, 3.5->4.0, 5->4
+    pts = {0.25: 0, 0.75: 2, 1.25: 2, 1.75: 4, 2.5: 4, 3.5: 6, 5.0: 6, 7.0: 7, 0.26: 1, 5.01: 7}
+    for v, c in pts.items():
+        assert O.lib.or_e2m1_encode_rne(v) == c, v
+        assert O.lib.or_e2m1_encode_rne(-v) == c | 8
+    assert O.lib.or_e2m1_encode_rne(-0.1) == 8  # sign kept on zero
+
+
+def test_nvfp4_reference_hand_made_block():
+    # tests/stream_tests.cu:1093-1107: amax 2688 = 448 * 6 gives global scale 1 and block scale 448 exactly
+    row = [2688, 112, 336, 560, 784, 1120, 1568, 2240, 113, -336, -10, 0, -2688, 338, -1568, 448] + [0] * 16
+    w = O.f32_to_bf16(np.array(row, np.float32)).reshape(1, 32)
+    v, s, g, _ = O.quant_nvfp4(w)
+    want = [7, 0, 1, 2, 3, 4, 5, 6, 1, 9, 0, 0, 15, 2, 13, 2]
+    assert g == 1.0
+    assert list(s[0]) == [0x7E, 0x01]
+    got = [(v[0, i // 2] >> (4 * (i & 1))) & 15 for i in range(16)]
+    assert got == want
+    assert np.all(v[0, 8:] == 0)
+
+
+def test_nvfp4_gaussian_error_band():
+    # tests/stream_tests.cu:1111-1119: relative squared error of N(0, 0.02) in (0.007, 0.011)
+    w = O.normal_bf16(33, 0.02, (256, 1024))
+    _, _, _, err = O.quant_nvfp4(w)
+    assert 0.007 < err < 0.011
+
+
+def test_nvfp4_quantizer_matches_torch_recipe():
+    # bench/quant/drafter_variants.py:94-104 (nvfp4_codes) evaluated with torch ops here (not imported)
+    w = O.normal_bf16(7, 0.02, (32, 256))
+    v, s, g, _ = O.quant_nvfp4(w)
+    wt = torch.from_numpy(w.view(np.int16)).view(torch.bfloat16).float()
+    N, K = wt.shape
+    gt = (wt.abs().max() / (448.0 * 6.0)).item()
+    b = wt.reshape(N, K // 16, 16)
+    sc = (b.abs().amax(-1, keepdim=True) / 6.0 / gt).clamp(min=2 ** -9).to(torch.float8_e4m3fn)
+    sv = sc.float() * gt
+    bounds = torch.tensor([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0])
+    y = b / sv
+    idx = torch.bucketize(y.abs(), bounds, right=False)
+    codes = (idx.to(torch.uint8) | (((y < 0) & (idx > 0)).to(torch.uint8) << 3)).reshape(N, K)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).numpy()
+    assert np.float32(g) == np.float32(gt)
+    assert np.array_equal(s, sc.view(torch.uint8).reshape(N, K // 16).numpy())
+    assert np.array_equal(v, packed)
+
+
+def test_fp8_per_channel_matches_torch_recipe():
+    # bench/quant/drafter_variants.py:77-81 (fake_fp8) with torch ops
+    w = O.normal_f32(5, 0.02, (64, 512))
+    q, s = O.quant_fp8_per_channel(w)
+    wt = torch.from_numpy(w)
+    st = (wt.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12)
+    qt = (wt / st).to(torch.float8_e4m3fn)
+    assert np.array_equal(s, st[:, 0].numpy())
+    assert np.array_equal(q, qt.view(torch.uint8).numpy())
+    # the row maximum lands exactly on 448
+    assert np.all(np.max(q & 0x7F, axis=1) == 0x7E)
+
+
+def test_fp8_block_quantizers_reconstruct():
+    w = O.normal_f32(9, 0.02, (256, 384))
+    q, s = O.quant_fp8_block128(w)
+    deq = O.dequant_fp8_block128(q, s)
+    assert s.shape == (2, 3)
+    rel = np.abs(deq - w).max() / np.abs(w).max()
+    assert rel < 2 ** -4  # E4M3 keeps 3 mantissa bits
+    # each block's largest magnitude maps to code 0x7e (448)
+    for nb in range(2):
+        for kb in range(3):
+            blk = q[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128]
+            assert (blk & 0x7F).max() == 0x7E
+    x = O.normal_bf16(10, 1.0, (4, 256))
+    xq, xs = O.quant_act_fp8_g128(x)
+    xf = O.bf16_to_f32(x)
+    for m in range(4):
+        for kb in range(2):
+            assert xs[m, kb] == np.float32(np.abs(xf[m, kb * 128:(kb + 1) * 128]).max()) / np.float32(448)
+    zero = np.zeros((1, 128), np.uint16)
+    zq, zs = O.quant_act_fp8_g128(zero)
+    assert zs[0, 0] == 1.0 and np.all(zq == 0)
+
+
+def test_tiled_fp8_literal_positions():
+    # piece p = ((h*2+q)*8+g)*4+t of a 2048-byte block holds W[16*tile+g+8h][128*chunk+32t+16q .. +16]
+    N, K = 32, 256
+    n_idx, k_idx = np.meshgrid(np.arange(N), np.arange(K), indexing="ij")
+    w = ((n_idx * 7 + k_idx * 13) % 251).astype(np.uint8)
+    t = O.retile_fp8(w)
+    assert t.size == N * K
+    assert np.array_equal(t[0:16], w[0, 0:16])          # piece 0
+    assert np.array_equal(t[16:32], w[0, 32:48])        # piece 1: t=1
+    assert np.array_equal(t[64:80], w[1, 0:16])         # piece 4: g=1
+    assert np.array_equal(t[512:528], w[0, 16:32])      # piece 32: q=1
+    assert np.array_equal(t[1024:1040], w[8, 0:16])     # piece 64: h=1
+    assert np.array_equal(t[2048:2064], w[0, 128:144])  # block 1 = (tile 0, chunk 1)
+    assert np.array_equal(t[4096:4112], w[16, 0:16])    # block 2 = (tile 1, chunk 0)
+    assert np.array_equal(O.untile_fp8(t, N, K), w)
+
+
+def test_tiled_nvfp4_literal_positions_and_round_trip():
+    N, K = 32, 256
+    v = (np.arange(N * K // 2) % 253).astype(np.uint8).reshape(N, K // 2)
+    s = (np.arange(N * K // 16) % 97 + 0x28).astype(np.uint8).reshape(N, K // 16)
+    t = O.retile_nvfp4(v, s)
+    assert t.size == N * K // 2 + N * K // 16
+    assert np.array_equal(t[0:16], v[0, 0:16])                # slot 0: row 0, values 0..31
+    assert np.array_equal(t[16:32], v[0, 16:32])              # slot 1: t=1
+    assert np.array_equal(t[64:80], v[1, 0:16])               # slot 4: row 1
+    assert np.array_equal(t[1024:1026], s[0, 0:2])            # scales of slot 0
+    assert np.array_equal(t[1026:1028], s[0, 2:4])
+    assert np.array_equal(t[1152:1168], v[0, 64:80])          # block (tile 0, chunk 1)
+    v2, s2 = O.untile_nvfp4(t, N, K)
+    assert np.array_equal(v2, v) and np.array_equal(s2, s)
+
+
+def test_coded_blob_round_trip():
+    w = O.normal_bf16(21, 0.02, (32, 512))
+    v, s, g, _ = O.quant_nvfp4(w)
+    ok, table, code_of = O.scale_code_table(s)
+    assert ok
+    blob, raw = O.retile_nvfp4_coded(v, s, code_of)
+    N, K = 32, 512
+    C = K // 128
+    blocks = (N // 16) * C
+    assert blob.size == blocks * 1120
+    plain = O.retile_nvfp4(v, s)
+    for blk in range(blocks):
+        assert np.array_equal(blob[blk * 1024:(blk + 1) * 1024], plain[blk * 1152:blk * 1152 + 1024])
+        assert np.array_equal(raw[blk * 128:(blk + 1) * 128], plain[blk * 1152 + 1024:(blk + 1) * 1152])
+        codes = blob[blocks * 1024 + blk * 96: blocks * 1024 + (blk + 1) * 96]
+        for L in range(64):
+            lo = codes[2 * (L % 32) + (L // 32)]
+            hi = (codes[64 + L % 32] >> (4 * (L // 32))) & 15
+            f = int(lo) | (int(hi) << 8)
+            assert table[f & 63] == raw[blk * 128 + 2 * L]
+            assert table[f >> 6] == raw[blk * 128 + 2 * L + 1]
+    too_many = np.arange(65, dtype=np.uint8)
+    assert not O.scale_code_table(too_many)[0]
+
+
+def test_dequant_and_gemm_vs_float64():
+    M, N, K = 5, 48, 384
+    x = O.normal_bf16(1, 1.0, (M, K))
+    w = O.normal_f32(2, 0.02, (N, K))
+    q, s = O.quant_fp8_per_channel(w)
+    wd = O.dequant_fp8_pc(q, s)
+    # dequantized values are exactly e4m3 * s in FP32
+    e = np.array([O.lib.or_e4m3_decode(c) for c in range(256)], np.float32)
+    assert np.array_equal(wd, (e[q] * s[:, None]).astype(np.float32))
+    xf = O.bf16_to_f32(x)
+    y = O.gemm_f32(xf, wd)
+    y64 = xf.astype(np.float64) @ wd.astype(np.float64).T
+    assert np.abs(y - y64).max() <= 1e-5 * np.abs(y64).max()
+    yb = O.stream_fp8_pc_bf16(x, q, s)
+    assert np.array_equal(yb, O.f32_to_bf16(y))
+    # a transposed operand or a dropped scale fails this check
+    assert np.abs(O.gemm_f32(xf, e[q]) - y64).max() > 1e-2
+
+
+def test_nvfp4_dequant_matches_reference_product_order():
+    w = O.normal_bf16(3, 0.02, (16, 256))
+    v, s, g, _ = O.quant_nvfp4(w)
+    d = O.dequant_nvfp4(v, s, g)
+    e = np.array([O.lib.or_e4m3_decode(c) for c in range(256)], np.float32)
+    f4 = np.array([O.lib.or_e2m1_decode(c) for c in range(16)], np.float32)
+    codes = np.stack([v & 15, v >> 4], -1).reshape(16, 256)
+    sc = (e[s] * np.float32(g)).astype(np.float32)
+    want = (f4[codes] * np.repeat(sc, 16, axis=1)).astype(np.float32)
+    assert np.array_equal(d, want)
+
+
+def test_epilogues():
+    g = np.array([-3.0, -0.5, 0.0, 0.7, 9.0], np.float32)
+    u = np.array([1.0, 2.0, 3.0, -1.5, 0.25], np.float32)
+    h = O.bf16_to_f32(O.epi_silu_mul_bf16(g, u))
+    want = (g / (1 + np.exp(-g.astype(np.float64)))) * u
+    assert np.allclose(h, want, rtol=2 ** -8)
+    r = O.f32_to_bf16(np.array([1.0, -2.0, 0.5, 100.0, 0.0], np.float32))
+    y = O.bf16_to_f32(O.epi_residual_bf16(g, r))
+    assert np.allclose(y, g + O.bf16_to_f32(r), rtol=2 ** -8)
+
+
+def test_to_half_rows_closed_form():
+    x = O.normal_f32(4, 1.0, (4, 256))
+    x[1] = 0.0
+    x[2, 7] = 3.0e30
+    x[3, 255] = np.inf
+    xh, xinv = O.to_half_rows(x)
+    for m in range(4):
+        mx = np.abs(x[m]).max()
+        e = int(np.frexp(np.float32(mx))[1]) if (mx > 0 and np.isfinite(mx)) else 0
+        assert xinv[m] == np.float32(2.0 ** (e - 15))
+        want = torch.from_numpy((x[m] * np.float32(2.0 ** (15 - e))).astype(np.float32)).to(torch.float16)
+        assert np.array_equal(xh[m], want.view(torch.int16).numpy().view(np.uint16))
+
+
+def test_generator_is_portable():
+    a = O.normal_f32(0x4C510000, 1.0, 8)
+    b = O.normal_f32(0x4C510000, 1.0, 8)
+    assert np.array_equal(a, b)
+    big = O.normal_f32(123, 1.0, 200000)
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
