@@ -1,0 +1,372 @@
+"""Benchmark of the fused quantized GEMM path on one MI355X.
+
+Headline (BASELINE.json metric): the speculative-verify MLP at M = 17 rows (config 2): gate|up
+(K = 5120, N = 2 x 17408, FP8 per-channel) with the SiLU*mul epilogue, then down (K = 17408, N = 5120) with the
+BF16 residual add. A step is one such pass; `value` is algorithmic HBM bytes per second of the whole step.
+Weights rotate over copies totalling >= 1 GB so neither L2 nor the 256 MB MALL serves the next step's weights.
+Inputs are synthetic (seeded N(0,1) activations, N(0,0.02) weights quantized like the checkpoints).
+
+Also reported beside it (same JSON line): decode M = 1 (config 1), the NVFP4 drafter fc (config 3), the full M = 68
+decode-step weight pass (config 5), and the block-scaled prefill GEMM at M = 4096 (config 4) in TFLOP/s.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (ROOT, os.path.join(ROOT, "ling-engine_amd"), os.path.join(ROOT, "oracle")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+FP8_DENSE_TFLOPS = 5000.0   # MI355X dense FP8 MFMA, published (no sparsity)
+ROTATE_BYTES = 1 << 30
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default="", help="comma list of extra sections to run (default: all)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the current stream around individual launches."""
+
+    def __init__(self, torch, n):
+        self.torch = torch
+        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        self.i = 0
+
+    def start(self):
+        self.ev[self.i][0].record()
+
+    def stop(self):
+        self.ev[self.i][1].record()
+        self.i += 1
+
+    def mean_ms(self):
+        return sum(a.elapsed_time(b) for a, b in self.ev[:self.i]) / max(1, self.i)
+
+
+def fp8_weight(torch, L, N, K, seed, dev):
+    """Random E4M3 codes (no NaN) in the tiled layout plus per-channel scales ~ amax/448 of N(0, 0.02)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    codes = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev, generator=g)
+    codes = torch.where((codes & 0x7F) == 0x7F, torch.full_like(codes, 0x3C), codes)
+    tw = L.retile_fp8(codes)
+    del codes
+    s = torch.full((N,), 0.02 * 4.5 / 448.0, dtype=torch.float32, device=dev)
+    return tw, s
+
+
+def bench_verify_mlp(torch, L, O, args, dev):
+    """Config 2: M = 17; returns the result dict and the roofline of the gate|up kernel."""
+    import numpy as np
+    M, H, F = 17, 5120, 17408
+    # one weight set is quantized by the oracle recipe from N(0, 0.02) (real numerics for the check below);
+    # the rotation copies are byte copies of it.
+    per_set = 2 * F * H + H * F
+    copies = max(2, -(-ROTATE_BYTES // per_set))
+    log(f"[bench] verify MLP M={M}: {copies} weight copies x {per_set / 1e6:.1f} MB")
+    sets = []
+    for c in range(copies):
+        wg, sg = fp8_weight(torch, L, F, H, 100 + 3 * c, dev)
+        wu, su = fp8_weight(torch, L, F, H, 101 + 3 * c, dev)
+        wd, sd = fp8_weight(torch, L, H, F, 102 + 3 * c, dev)
+        sets.append((wg, sg, wu, su, wd, sd))
+    x = torch.from_numpy(O.normal_bf16(0x4C510002, 1.0, (M, H)).view(np.int16)).to(dev).view(torch.bfloat16)
+    r0 = torch.from_numpy(O.normal_bf16(0x4C510003, 1.0, (M, H)).view(np.int16)).to(dev).view(torch.bfloat16)
+    h = torch.empty((M, F), dtype=torch.bfloat16, device=dev)
+    r = r0.clone()
+
+    def step(i, tg=None, td=None):
+        wg, sg, wu, su, wd, sd = sets[i % copies]
+        if tg: tg.start()
+        L.stream_fp8_pc_silu_mul(x, wg, sg, wu, su, F, h=h)
+        if tg: tg.stop()
+        if td: td.start()
+        L.stream_fp8_pc_residual(h, wd, sd, r, H, y=r)
+        if td: td.stop()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    tg, td = Timer(torch, args.steps), Timer(torch, args.steps)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(args.steps):
+        step(i, tg, td)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    # algorithmic bytes: weights + scales + activations in/out (+ residual read and write)
+    b_gu = 2 * F * H + 2 * F * 4 + M * H * 2 + M * F * 2
+    b_dn = H * F + H * 4 + M * F * 2 + 2 * M * H * 2
+    gb_s = (b_gu + b_dn) / (ms * 1e-3) / 1e9
+    gu_ms, dn_ms = tg.mean_ms(), td.mean_ms()
+    res = {
+        "ms_per_step": ms,
+        "gb_s": gb_s,
+        "bytes_per_step": b_gu + b_dn,
+        "gate_up": {"ms": gu_ms, "bytes": b_gu, "gb_s": b_gu / (gu_ms * 1e-3) / 1e9},
+        "down": {"ms": dn_ms, "bytes": b_dn, "gb_s": b_dn / (dn_ms * 1e-3) / 1e9},
+        "rotation_copies": copies,
+    }
+    del sets
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_skinny(torch, L, O, args, dev, name, M, N, K, fmt):
+    """A single skinny GEMM over rotating copies: returns ms per launch and GB/s."""
+    import numpy as np
+    if fmt == "fp8":
+        wbytes, sbytes = N * K, N * 4
+    else:
+        wbytes, sbytes = N * K // 2 + N * K // 16, 0
+    copies = max(2, -(-ROTATE_BYTES // wbytes))
+    ws = []
+    for c in range(copies):
+        if fmt == "fp8":
+            ws.append(fp8_weight(torch, L, N, K, 200 + c, dev))
+        else:
+            g = torch.Generator(device=dev)
+            g.manual_seed(300 + c)
+            v = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g)
+            s = torch.randint(0x28, 0x48, (N, K // 16), dtype=torch.uint8, device=dev, generator=g)
+            ws.append((L.retile_nvfp4(v, s), None))
+            del v, s
+    x = torch.from_numpy(O.normal_bf16(0x4C510000 + M, 1.0, (M, K)).view(np.int16)).to(dev).view(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def run(i):
+        w, s = ws[i % copies]
+        if fmt == "fp8":
+            L.stream_fp8_pc(x, w, s, N, y=y)
+        else:
+            L.stream_nvfp4_bf16(x, w, None, 1e-3, N, y=y)
+
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for i in range(args.steps):
+        run(i)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    b = wbytes + sbytes + M * K * 2 + M * N * 2
+    del ws
+    torch.cuda.empty_cache()
+    return {"M": M, "N": N, "K": K, "format": fmt, "ms": ms, "bytes": b, "gb_s": b / (ms * 1e-3) / 1e9,
+            "frac_hbm": b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_decode_step(torch, L, O, args, dev):
+    """Config 5: M = 68 through 64 layers (48 DeltaNet, 16 attention, 64 MLP) + lm_head, FP8 per-channel."""
+    import numpy as np
+    M, H, F = 68, 5120, 17408
+    mats = []  # (kind, N, K): kind "plain", "silu" (pairs), "resid"
+    for li in range(64):
+        if li % 4 == 3:
+            mats += [("plain", 7168, H), ("resid", H, 6144)]
+        else:
+            mats += [("plain", 12352, H), ("resid", H, 6144)]
+        mats += [("silu", F, H), ("resid", H, F)]
+    mats.append(("plain", 151936, H))
+    total = 0
+    weights = []
+    for i, (kind, N, K) in enumerate(mats):
+        n_mats = 2 if kind == "silu" else 1
+        ws = [fp8_weight(torch, L, N, K, 1000 + 2 * i + j, dev) for j in range(n_mats)]
+        total += n_mats * (N * K + N * 4)
+        weights.append(ws)
+    xs = {K: torch.from_numpy(O.normal_bf16(0x4C510005 + K, 1.0, (M, K)).view(np.int16)).to(dev).view(torch.bfloat16)
+          for K in (H, 6144, F)}
+    ys = {}
+
+    def out(N):
+        if N not in ys:
+            ys[N] = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+        return ys[N]
+
+    def step():
+        for (kind, N, K), ws in zip(mats, weights):
+            if kind == "plain":
+                L.stream_fp8_pc(xs[K], ws[0][0], ws[0][1], N, y=out(N))
+            elif kind == "silu":
+                L.stream_fp8_pc_silu_mul(xs[K], ws[0][0], ws[0][1], ws[1][0], ws[1][1], N, h=out(N))
+            else:
+                r = out(N)
+                L.stream_fp8_pc_residual(xs[K], ws[0][0], ws[0][1], r, N, y=r)
+
+    steps = max(1, min(args.steps // 20, 10))
+    step()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    del weights
+    torch.cuda.empty_cache()
+    return {"M": M, "launches": len(mats), "weight_bytes": total, "ms": ms, "gb_s": total / (ms * 1e-3) / 1e9,
+            "frac_hbm": total / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "steps": steps}
+
+
+def bench_prefill(torch, L, O, args, dev):
+    """Config 4: M = 4096 FP8 x FP8 block-scaled GEMMs (gate|up as one N = 34816 GEMM, down), BF16 out."""
+    if not hasattr(L, "prefill_fp8_block"):
+        return None
+    M, H, F = 4096, 5120, 17408
+    res = {}
+    total_flop, total_ms = 0.0, 0.0
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    xq = {}
+    for name, N, K in (("gate_up", 2 * F, H), ("down", H, F)):
+        codes = torch.randint(0, 256, (N, K), dtype=torch.uint8, device=dev, generator=g)
+        codes = torch.where((codes & 0x7F) == 0x7F, torch.full_like(codes, 0x3C), codes)
+        w = L.retile_fp8(codes)
+        del codes
+        ws = torch.rand((N // 128, K // 128), dtype=torch.float32, device=dev, generator=g) * 1e-3 + 1e-4
+        a = torch.randint(0, 256, (M, K), dtype=torch.uint8, device=dev, generator=g)
+        a = torch.where((a & 0x7F) == 0x7F, torch.full_like(a, 0x3C), a)
+        xs = torch.rand((M, K // 128), dtype=torch.float32, device=dev, generator=g) * 1e-2 + 1e-3
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        steps = max(5, args.steps // 10)
+        for _ in range(3):
+            L.prefill_fp8_block(a, xs, w, ws, N, y=y)
+        torch.cuda.synchronize()
+        tm = Timer(torch, steps)
+        for _ in range(steps):
+            tm.start()
+            L.prefill_fp8_block(a, xs, w, ws, N, y=y)
+            tm.stop()
+        torch.cuda.synchronize()
+        ms = tm.mean_ms()
+        flop = 2.0 * M * N * K
+        res[name] = {"M": M, "N": N, "K": K, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+                     "frac_mfma": flop / (ms * 1e-3) / 1e12 / FP8_DENSE_TFLOPS}
+        total_flop += flop
+        total_ms += ms
+        del w, a, xs, y
+    res["total"] = {"flop": total_flop, "ms": total_ms, "tflops": total_flop / (total_ms * 1e-3) / 1e12,
+                    "frac_mfma": total_flop / (total_ms * 1e-3) / 1e12 / FP8_DENSE_TFLOPS}
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(O):
+    """The oracle's whole CPU path (dequantize to FP32, FP32 accumulate, BF16 out) on a bounded sample of config 2:
+    all 17 rows against the first `n` output channels of gate|up, on every host core; scaled to GB/s."""
+    M, H, F = 17, 5120, 17408
+    threads = O.hardware_threads()
+    x = O.normal_bf16(0x4C510002, 1.0, (M, H))
+    w = O.normal_f32(0x4C510004, 0.02, (2048, H))
+    q, s = O.quant_fp8_per_channel(w)
+    # grow the sample until one pass takes >= ~2 s, then time 3 passes and keep the best
+    n = 256
+    while True:
+        t = time.perf_counter()
+        O.stream_fp8_pc_bf16(x, q[:n], s[:n], 0, n, threads)
+        dt = time.perf_counter() - t
+        if dt >= 2.0 or n >= 2048:
+            break
+        n = min(2048, n * 2)
+    best = dt
+    for _ in range(2):
+        t = time.perf_counter()
+        O.stream_fp8_pc_bf16(x, q[:n], s[:n], 0, n, threads)
+        best = min(best, time.perf_counter() - t)
+    b = n * H + n * 4 + M * H * 2 + M * n * 2
+    return {"value": b / best / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"M={M}, K={H}, first {n} of 34816 gate|up output channels (FP8 per-channel), best of 3, "
+                      f"{best:.2f} s per pass"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the path is single-GPU); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import ling_gemm as L
+    import oracle as O
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    L.init()
+    only = set(args.only.split(",")) if args.only else None
+    props = torch.cuda.get_device_properties(0)
+    log(f"[bench] {props.name} CUs={props.multi_processor_count} mem={props.total_memory / 2**30:.0f} GiB")
+
+    vm = bench_verify_mlp(torch, L, O, args, dev)
+    log(f"[bench] verify MLP: {vm['ms_per_step'] * 1e3:.1f} us/step, {vm['gb_s']:.0f} GB/s")
+    extra = {}
+    if only is None or "decode" in only:
+        extra["decode_m1"] = bench_skinny(torch, L, O, args, dev, "decode", 1, 5120, 5120, "fp8")
+        log(f"[bench] decode M=1: {extra['decode_m1']}")
+    if only is None or "nvfp4" in only:
+        extra["drafter_fc_nvfp4_m16"] = bench_skinny(torch, L, O, args, dev, "fc", 16, 5120, 25600, "nvfp4")
+        log(f"[bench] nvfp4 fc: {extra['drafter_fc_nvfp4_m16']}")
+    if only is None or "step" in only:
+        extra["decode_step_m68"] = bench_decode_step(torch, L, O, args, dev)
+        log(f"[bench] full step M=68: {extra['decode_step_m68']}")
+    if only is None or "prefill" in only:
+        pf = bench_prefill(torch, L, O, args, dev)
+        if pf:
+            extra["prefill_m4096"] = pf
+            log(f"[bench] prefill: {pf['total']}")
+    cpu = None if args.no_cpu else cpu_baseline(O)
+    if cpu:
+        log(f"[bench] cpu baseline: {cpu}")
+
+    gu = vm["gate_up"]
+    line = {
+        "metric": "verify GEMM HBM GB/s (% peak) at M=17; prefill block-scaled TFLOP/s",
+        "value": round(vm["gb_s"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(vm["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) BF16 activations; random FP8 E4M3 weight codes, per-channel scales)",
+        "config": {"workload": "speculative-verify MLP, M=17: gate|up 5120->2x17408 FP8 per-channel + SiLU*mul, "
+                               "down 17408->5120 + BF16 residual (BASELINE config 2)",
+                   "M": 17, "hidden": 5120, "ffn": 17408, "weight_format": "fp8_e4m3 per-channel",
+                   "rotation_copies": vm["rotation_copies"]},
+        "frac_hbm": round(vm["gb_s"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gu["gb_s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu["gb_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "stream_kernel (gate|up + SiLU*mul, M=17)", "bytes_per_launch": gu["bytes"],
+                     "ms_per_launch": round(gu["ms"], 5)},
+        "kernels": {"gate_up_silu": gu, "down_residual": vm["down"]},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

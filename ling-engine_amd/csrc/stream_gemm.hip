@@ -3,24 +3,28 @@
 //   y[m][n] = epilogue( sum_k x[m][k] * Wq[n][k] ),  Wq = FP8 E4M3 or NVFP4 (E2M1 x E4M3 block scale) codes
 //
 // The weights are read once from HBM in the reference's tiled layout (a 16-row x 128-value block is
-// contiguous); everything else (activations, partial sums) stays in the caches. Design points:
+// contiguous); activations and partial sums stay on chip or in the caches. Design:
 //
 //  * MFMA v_mfma_f32_16x16x32_{bf16,f16}: A = 16 weight rows x 32 K, B = 32 K x 16 activation rows.
 //    Lane l (r = l % 16, t = l / 16) owns weight row r of a tile and K range [32t, 32t + 32) of each
 //    128-value chunk. An FP8 block's 16-byte pieces for that row/range sit at ((h*2+q)*8+g)*4+t
 //    (g = r % 8, h = r / 8, q = 0, 1) and an NVFP4 block's at slot r*4+t, so each load instruction of the
 //    wave covers whole 512-byte (FP8) or 1024-byte (NVFP4) runs of the block. The MFMA's logical k of
-//    step s maps to physical K 32t + 8s + j for the weights and the activations alike, so the dot
-//    product is unchanged.
+//    step s maps to physical K 32t + 8s + j for the weights and the activations alike.
 //  * Dequantization in registers, exact: FP8 -> BF16/FP16 with v_cvt_scalef32_pk_*_fp8 (scale 1.0);
 //    NVFP4 -> FP16 with v_cvt_scalef32_pk_f16_fp4 (scale 1.0) then one v_pk_mul_f16 by the E4M3 block
 //    scale (e2m1 * e4m3 has at most 5 significant bits: exact in FP16). The per-channel / global scale
 //    is applied in FP32 in the epilogue.
-//  * Work split: units = (tile group of kTiles tiles, K chunk); P workgroups each take a contiguous,
-//    equal range of units (a stream-K split), so every CU streams the same number of bytes whatever
-//    N and K are. Within a workgroup, wave w takes chunks c0 + w, c0 + w + kWaves, ... and the waves'
-//    sums are added in LDS in wave order. A tile group split across workgroups is finished by the last
-//    workgroup to arrive (an arrival counter per group), which adds the partial sums in workgroup order.
+//  * A workgroup is 4 waves over a tile group of 16 tiles (256 weight rows); wave w owns tiles
+//    4w .. 4w + 3 and all waves walk the same K chunks in lock step. Each chunk's activations are staged
+//    once per workgroup in LDS (each wave loads a quarter; 16-byte units XOR-swizzled by row so the
+//    MFMA operand reads are conflict free), while each wave streams its own weights through a ring of PF
+//    chunks in registers. Loads retire in issue order, so a chunk's activation share is issued before its
+//    weights and the stages are consumed oldest first: every wait leaves the newer stages in flight.
+//  * Work split: units = (tile group, K chunk); P workgroups each take a contiguous, equal range of
+//    units (a stream-K split), so every CU streams the same number of bytes whatever N and K are. A tile
+//    group split across workgroups is finished by the last workgroup to arrive (an arrival counter per
+//    group), which adds the partial sums in workgroup order and applies the epilogue.
 //  * Determinism and row invariance: P, the tile grouping and the chunk order depend only on N, K and
 //    the device's CU count, never on M, and an MFMA's column j depends only on activation row j; so a
 //    row's result is bit for bit the same at any M, as the reference guarantees
@@ -31,18 +35,28 @@
 #include "lq_workspace.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
 namespace lq {
 namespace {
 
-constexpr int kTiles = 4;  // 16-row tiles per tile group (64 weight rows)
-constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kWaves = 4;  // waves per workgroup, one per tile slot of the tile group
 constexpr int kThreads = kWaves * kWave;
+// 16-row tiles per wave: one, or one gate and one up tile with the SiLU*mul epilogue. A tile group is the
+// workgroup's 4 waves' tiles: 64 output rows.
+template <bool PAIR>
+constexpr int tiles_per_wave() { return PAIR ? 2 : 1; }
+constexpr int kGroupRows = 64;  // output rows (columns of y) per tile group
 constexpr int kMaxMats = 4;
 
+
 enum WFmt { kFp8 = 0, kFp4 = 1, kFp4Coded = 2 };
+
+// Weight chunks in flight per wave (the computed one included), by register budget.
+template <int T>
+__host__ __device__ constexpr int pf_stages(int G) { return T == 1 ? (G <= 2 ? 8 : G <= 4 ? 6 : 4) : (G <= 2 ? 6 : 4); }
 
 struct StreamArgs {
   const void* x;      // [M][K] BF16 or FP16
@@ -53,73 +67,62 @@ struct StreamArgs {
   int TG;             // tile groups
   int count;          // matrices
   const uint8_t* w[kMaxMats];
-  const uint8_t* table[kMaxMats];  // coded NVFP4: device scale-code table [64]
-  const float* svec[kMaxMats];     // per-channel scales [N] or null
-  float sc[kMaxMats];              // scalar scale (used when svec is null)
-  void* y[kMaxMats];               // BF16 or FP32 [M][ldy]
-  const uint16_t* resid[kMaxMats]; // BF16 residual [M][ldy] or null
+  const uint8_t* table[kMaxMats];   // coded NVFP4: device scale-code table [64]
+  const float* svec[kMaxMats];      // per-channel scales [N] or null
+  float sc[kMaxMats];               // scalar scale (used when svec is null)
+  void* y[kMaxMats];                // BF16 or FP32 [M][ldy]
+  const uint16_t* resid[kMaxMats];  // BF16 residual [M][ldy] or null
   int N[kMaxMats];
   int tg0[kMaxMats + 1];  // first tile group of each matrix; tg0[count] = TG
   int ldy[kMaxMats];
-  float* partials;  // [2 * P][kTiles * 16][G * 16]
+  float* partials;  // [2 * P][T * G * 4][256] per workgroup slot
   int* counters;    // [TG]
 };
 
 // One chunk of weights for the lane: FP8 32 bytes (two pieces) per tile; NVFP4 16 bytes + 2 scales.
-template <int WF>
+template <int WF, int T>
 struct WRegs {
-  u32x4 v[kTiles][WF == kFp8 ? 2 : 1];
-  uint32_t sc[kTiles];  // NVFP4: the two E4M3 block scales (raw) or the 12-bit code (coded)
+  u32x4 v[T][WF == kFp8 ? 2 : 1];
+  uint32_t sc[T];  // NVFP4: the two E4M3 block scales (raw) or the 12-bit code pair (coded)
 };
 
-template <int G>
-struct XRegs {
-  u32x4 v[G][4];  // 4 x 8 activations = K [32t, 32t + 32) of row 16g + r
-};
+// Buffer resources: a raw (stride 0) descriptor per matrix; lane offsets in one VGPR, the tile/chunk offset
+// in an SGPR, so the ring of in-flight loads costs no address registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+constexpr int kNT = 2;  // slc: streaming (non-temporal) weights
 
-template <int WF>
-__device__ __forceinline__ void load_w(WRegs<WF>& R, const uint8_t* const (&tb)[kTiles], const uint8_t* const (&cb)[kTiles],
-                                       int c, int lane) {
-  const int r = lane & 15, t = lane >> 4;
+template <int WF, int T>
+__device__ __forceinline__ void load_w(WRegs<WF, T>& R, const __amdgpu_buffer_rsrc_t (&rs)[T], const int (&toff)[T],
+                                       const int (&coff)[T], int c, int lane_off, int slot, unsigned oob) {
 #pragma unroll
-  for (int i = 0; i < kTiles; ++i) {
+  for (int i = 0; i < T; ++i) {
     if constexpr (WF == kFp8) {
-      const int p0 = ((r >> 3) * 16 + (r & 7)) * 4 + t;  // piece of q = 0; q = 1 is 32 pieces on
-      const uint8_t* b = tb[i] + static_cast<size_t>(c) * kTileBytesFp8 + p0 * 16;
-      R.v[i][0] = load_nt(b);
-      R.v[i][1] = load_nt(b + 512);
+      const int so = toff[i] + c * kTileBytesFp8;
+      R.v[i][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[i], lane_off, so, kNT));
+      R.v[i][1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[i], lane_off + 512, so, kNT));
     } else if constexpr (WF == kFp4) {
-      const int s = r * 4 + t;
-      const uint8_t* b = tb[i] + static_cast<size_t>(c) * kTileBytesFp4;
-      R.v[i][0] = load_nt(b + s * 16);
-      R.sc[i] = *reinterpret_cast<const uint16_t*>(b + 1024 + s * 2);
+      const int so = toff[i] + c * kTileBytesFp4;
+      R.v[i][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[i], lane_off, so, kNT));
+      R.sc[i] = static_cast<uint16_t>(
+          __builtin_amdgcn_raw_buffer_load_b16(rs[i], static_cast<int>((1024 + 2 * slot) | oob), so, 0));
     } else {
-      const int s = r * 4 + t;
-      const uint8_t* b = tb[i] + static_cast<size_t>(c) * kValueBytesFp4;
-      R.v[i][0] = load_nt(b + s * 16);
+      const int so = toff[i] + c * kValueBytesFp4;
+      R.v[i][0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[i], lane_off, so, kNT));
       // slot s < 32: low byte at 2s, high nibble in the low half of byte 64 + s; slot 32 + L: byte 2L + 1
       // and the high half of byte 64 + L (reference src/core/stream_gemm.cu:740-780).
-      const uint8_t* cd = cb[i] + static_cast<size_t>(c) * kCodeBytesFp4;
-      const int L = s & 31, hi = s >> 5;
-      const uint32_t lo = cd[2 * L + hi], nib = (cd[64 + L] >> (4 * hi)) & 15u;
-      R.sc[i] = lo | (nib << 8);
+      const int L = slot & 31, hi = slot >> 5, cso = coff[i] + c * kCodeBytesFp4;
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b8(rs[i], static_cast<int>((2 * L + hi) | oob), cso, 0);
+      const uint32_t nb = __builtin_amdgcn_raw_buffer_load_b8(rs[i], static_cast<int>((64 + L) | oob), cso, 0);
+      R.sc[i] = lo | (((nb >> (4 * hi)) & 15u) << 8);
     }
   }
 }
 
-template <int G>
-__device__ __forceinline__ void load_x(XRegs<G>& X, const uint8_t* const (&xrow)[G], int c) {
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const uint8_t* p = xrow[g] + static_cast<size_t>(c) * (kChunk * 2);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) X.v[g][s] = load16(p + 16 * s);
-  }
-}
-
 // The A operand of MFMA step s (8 weights, K 32t + 8s .. +8) for tile i.
-template <int WF, bool F16>
-__device__ __forceinline__ u32x4 a_operand(const WRegs<WF>& R, int i, int s, const uint8_t* tab) {
+template <int WF, bool F16, int T>
+__device__ __forceinline__ u32x4 a_operand(const WRegs<WF, T>& R, int i, int s, const uint8_t* tab) {
   if constexpr (WF == kFp8) {
     const u32x4& v = R.v[i][s >> 1];
     const uint32_t d0 = (s & 1) ? v.z : v.x, d1 = (s & 1) ? v.w : v.y;
@@ -127,7 +130,7 @@ __device__ __forceinline__ u32x4 a_operand(const WRegs<WF>& R, int i, int s, con
     const u32x2 b = F16 ? fp8x4_to_f16x4(d1) : fp8x4_to_bf16x4(d1);
     return u32x4{a.x, a.y, b.x, b.y};
   } else {
-    // the two block scales (K [32t, +16) and [32t + 16, +32)); s < 2 uses the first
+    // the two block scales (K [32t, +16) and [32t + 16, +32)); steps 0, 1 use the first
     uint32_t scb;
     if constexpr (WF == kFp4) scb = (s < 2) ? (R.sc[i] & 0xffu) : (R.sc[i] >> 8);
     else scb = tab[(s < 2) ? (R.sc[i] & 63u) : (R.sc[i] >> 6)];
@@ -140,43 +143,94 @@ __device__ __forceinline__ u32x4 a_operand(const WRegs<WF>& R, int i, int s, con
   }
 }
 
-template <int WF, bool F16, int G>
-__device__ __forceinline__ void compute(const WRegs<WF>& R, const XRegs<G>& X, f32x4 (&acc)[kTiles][G],
-                                        const uint8_t* const (&tab)[kTiles]) {
+// LDS image of one chunk of activations: row m's 16 units of 16 bytes (8 values), unit u at (u ^ (m & 15)).
+__device__ __forceinline__ int xs_off(int row, int unit) { return row * 256 + ((unit ^ (row & 15)) << 4); }
+
+// Accumulators are split by MFMA step parity (two independent chains per output tile and row group), so
+// consecutive MFMAs never wait on each other's results; the two halves are added once per segment.
+template <int WF, bool F16, int G, int T>
+__device__ __forceinline__ void mfma_step(const WRegs<WF, T>& R, int s, const u32x4 (&b)[G], f32x4 (&acc)[2][T][G],
+                                          const uint8_t* const (&tab)[T]) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
+  for (int i = 0; i < T; ++i) {
+    const u32x4 a = a_operand<WF, F16, T>(R, i, s, tab[i]);
 #pragma unroll
-    for (int i = 0; i < kTiles; ++i) {
-      const u32x4 a = a_operand<WF, F16>(R, i, s, tab[i]);
+    for (int g = 0; g < G; ++g) acc[s & 1][i][g] = mfma16x16x32(a, b[g], acc[s & 1][i][g], F16);
+  }
+}
+
+template <int G>
+__device__ __forceinline__ void read_b(u32x4 (&b)[G], const uint8_t* xs, int s, int r, int t) {
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[i][g] = mfma16x16x32(a, X.v[g][s], acc[i][g], F16);
-    }
+  for (int g = 0; g < G; ++g) b[g] = *reinterpret_cast<const u32x4*>(xs + xs_off(16 * g + r, 4 * t + s));
+}
+
+// One chunk with the activation operands read from LDS inside (the next step's while the current computes).
+template <int WF, bool F16, int G, int T>
+__device__ __forceinline__ void compute_lds(const WRegs<WF, T>& R, const uint8_t* xs, f32x4 (&acc)[2][T][G], int r,
+                                            int t, const uint8_t* const (&tab)[T]) {
+  u32x4 b[2][G];
+  read_b<G>(b[0], xs, 0, r, t);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s < 3) read_b<G>(b[(s + 1) & 1], xs, s + 1, r, t);
+    mfma_step<WF, F16, G, T>(R, s, b[s & 1], acc, tab);
+  }
 }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
-// Applies the epilogue to one reduced sum and stores it. `row` is the tile group's row (0 .. 63).
-template <bool PAIR, bool OUTF32, int G>
-__device__ __forceinline__ void epilogue_store(const StreamArgs& a, int mi, int tile0, float (*red)[G * 16 + 1],
-                                               int row, int tok) {
-  if constexpr (PAIR) {
-    const int n = tile0 * 16 + row;  // gate / up column
-    if (n >= a.N[0]) return;
-    const float g = red[row][tok], u = red[row + kTiles * 8][tok];
-    const float gs = g * (a.svec[0] ? a.svec[0][n] : a.sc[0]);
-    const float us = u * (a.svec[1] ? a.svec[1][n] : a.sc[1]);
-    reinterpret_cast<uint16_t*>(a.y[0])[static_cast<size_t>(tok) * a.ldy[0] + n] = f32_to_bf16(silu(gs) * us);
-  } else {
-    const int n = tile0 * 16 + row;
-    if (n >= a.N[mi]) return;
-    float v = red[row][tok] * (a.svec[mi] ? a.svec[mi][n] : a.sc[mi]);
-    if (a.xinv) v = v * a.xinv[tok];
-    const size_t o = static_cast<size_t>(tok) * a.ldy[mi] + n;
-    if constexpr (OUTF32) {
-      reinterpret_cast<float*>(a.y[mi])[o] = v;
+// Epilogue of one lane's outputs: acc[i][g][v] is row 16 * tile(i) + 4t + v, token 16g + r.
+template <int G, bool PAIR, bool OUTF32, int T = tiles_per_wave<PAIR>()>
+__device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0, const f32x4 (&acc)[T][G], int r,
+                                         int t) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int tok = 16 * g + r;
+    if (tok >= a.M) continue;
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int i = 0; i < T / 2; ++i) {
+        const int n = (wtile0 + i) * 16 + 4 * t;
+        if (n >= a.N[0]) continue;
+        uint16_t o[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float gs = acc[i][g][v] * (a.svec[0] ? a.svec[0][n + v] : a.sc[0]);
+          const float us = acc[i + T / 2][g][v] * (a.svec[1] ? a.svec[1][n + v] : a.sc[1]);
+          o[v] = f32_to_bf16(silu(gs) * us);
+        }
+        uint16_t* dst = reinterpret_cast<uint16_t*>(a.y[0]) + static_cast<size_t>(tok) * a.ldy[0] + n;
+        *reinterpret_cast<u32x2*>(dst) = u32x2{o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16)};
+      }
     } else {
-      if (a.resid[mi]) v = v + bf16_to_f32(a.resid[mi][o]);
-      reinterpret_cast<uint16_t*>(a.y[mi])[o] = f32_to_bf16(v);
+      const float xi = a.xinv ? a.xinv[tok] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < T; ++i) {
+        const int n = (wtile0 + i) * 16 + 4 * t;
+        if (n >= a.N[mi]) continue;
+        float vv[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          vv[v] = acc[i][g][v] * (a.svec[mi] ? a.svec[mi][n + v] : a.sc[mi]);
+          if (a.xinv) vv[v] = vv[v] * xi;
+        }
+        const size_t o = static_cast<size_t>(tok) * a.ldy[mi] + n;
+        if constexpr (OUTF32) {
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.y[mi]) + o) = f32x4{vv[0], vv[1], vv[2], vv[3]};
+        } else {
+          if (a.resid[mi]) {
+            const u32x2 rr = *reinterpret_cast<const u32x2*>(a.resid[mi] + o);
+            vv[0] = vv[0] + bf16_to_f32(rr.x & 0xffff);
+            vv[1] = vv[1] + bf16_to_f32(rr.x >> 16);
+            vv[2] = vv[2] + bf16_to_f32(rr.y & 0xffff);
+            vv[3] = vv[3] + bf16_to_f32(rr.y >> 16);
+          }
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.y[mi]) + o) =
+              u32x2{f32_to_bf16(vv[0]) | (uint32_t(f32_to_bf16(vv[1])) << 16),
+                    f32_to_bf16(vv[2]) | (uint32_t(f32_to_bf16(vv[3])) << 16)};
+        }
+      }
     }
   }
 }
@@ -188,11 +242,19 @@ __device__ __forceinline__ long long unit_start(int p, int P, long long U) { ret
 
 template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
-  constexpr int ROWS = kTiles * 16, COLS = G * 16;
-  __shared__ float red[ROWS][COLS + 1];
+  constexpr int T = tiles_per_wave<PAIR>();
+  constexpr int PF = pf_stages<T>(G);
+  // G <= 2: a chunk's activation operands (all four steps) are read from LDS one chunk ahead, into registers,
+  // through a ring of three LDS slots; larger G reads them within the chunk from a ring of two.
+  constexpr bool BPRE = G <= 2;
+  constexpr int NSLOT = BPRE ? 3 : 2;
+  constexpr int XS_BYTES = 16 * G * 256;  // one chunk of activations, 16G rows
+  constexpr int NACC = T * G * 4;          // accumulator floats per lane
+  static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
+  __shared__ __attribute__((aligned(16))) uint8_t xs[NSLOT][XS_BYTES];
   __shared__ uint8_t tabs[kMaxMats][64];
   __shared__ int last_flag;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, t = lane >> 4;
 
   if constexpr (WF == kFp4Coded) {
@@ -207,115 +269,199 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   const long long u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
   const int tg_first = static_cast<int>(u0 / a.C);
 
-  // Activation row pointers of this lane (rows past M read row M - 1; their columns are never stored).
-  const uint8_t* xrow[G];
+  // This thread's share of a chunk's activations: units q = i * 256 + tid of the 16G x 16 units (row q / 16,
+  // 16-byte unit q % 16). Rows past M read as zeros from out-of-range offsets (their MFMA columns are never
+  // stored).
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x);
+  int xsrc[G], xdst[G];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const int m = min(16 * g + r, a.M - 1);
-    xrow[g] = reinterpret_cast<const uint8_t*>(a.x) + (static_cast<size_t>(m) * a.K + 32 * t) * 2;
+  for (int i = 0; i < G; ++i) {
+    const int q = i * kThreads + static_cast<int>(threadIdx.x), row = q >> 4, u = q & 15;
+    xsrc[i] = row < a.M ? (row * a.K) * 2 + u * 16 : static_cast<int>(0x80000000u);
+    xdst[i] = xs_off(row, u);
   }
+  // weight lane offset: FP8 piece ((h*2 + 0)*8 + g)*4 + t (q = 1 is 512 bytes on); NVFP4 slot r*4 + t
+  const int slot = r * 4 + t;
+  const int lane_off = WF == kFp8 ? (((r >> 3) * 16 + (r & 7)) * 4 + t) * 16 : slot * 16;
 
-  for (long long u = u0; u < u1;) {
-    const int tg = static_cast<int>(u / a.C), c0 = static_cast<int>(u % a.C);
-    const int c1 = static_cast<int>(min(static_cast<long long>(a.C), c0 + (u1 - u)));
-    u += c1 - c0;
+  // The range's segments (one per tile group it touches), the split ones first: a split tile group's other
+  // workgroups also process their share of it first, so its reduction happens early, not at the kernel's end.
+  const int nseg = u1 > u0 ? static_cast<int>((u1 - 1) / a.C) - tg_first + 1 : 0;
+  const bool tail_split = nseg > 1 && (u1 % a.C) != 0;
+  for (int k = 0; k < nseg; ++k) {
+    const int sidx = tail_split ? (k == 0 ? nseg - 1 : k - 1) : k;
+    const int tg = tg_first + sidx;
+    const int c0 = sidx == 0 ? static_cast<int>(u0 % a.C) : 0;
+    const int c1 = static_cast<int>(min(static_cast<long long>(a.C), u1 - static_cast<long long>(tg) * a.C));
 
-    // The tile group's tiles: PAIR = kTiles/2 gate tiles then the same up tiles; else kTiles tiles of one matrix.
+    // This wave's tiles: PAIR = gate tile wtile0 then the same up tile; else tile wtile0 of one matrix.
     int mi = 0;
     if constexpr (!PAIR) {
       while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
     }
-    const int tile0 = PAIR ? tg * (kTiles / 2) : (tg - a.tg0[mi]) * kTiles;
-    const uint8_t* tb[kTiles];
-    const uint8_t* cb[kTiles];
-    const uint8_t* tab[kTiles];
+    const int wtile0 = (tg - a.tg0[mi]) * (kGroupRows / 16) + wave * (PAIR ? T / 2 : T);
+    __amdgpu_buffer_rsrc_t rs[T];
+    int toff[T], coff[T];
+    const uint8_t* tab[T];
 #pragma unroll
-    for (int i = 0; i < kTiles; ++i) {
-      const int m = PAIR ? (i < kTiles / 2 ? 0 : 1) : mi;
-      const int tile = min((PAIR ? tile0 + (i % (kTiles / 2)) : tile0 + i), a.N[m] / 16 - 1);
-      const size_t blk = WF == kFp8 ? kTileBytesFp8 : WF == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
-      tb[i] = a.w[m] + static_cast<size_t>(tile) * a.C * blk;
-      cb[i] = a.w[m] + static_cast<size_t>(a.N[m] / 16) * a.C * kValueBytesFp4 +
-              static_cast<size_t>(tile) * a.C * kCodeBytesFp4;
+    for (int i = 0; i < T; ++i) {
+      const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
+      const int tile = min((PAIR ? wtile0 + (i % (T / 2)) : wtile0 + i), a.N[m] / 16 - 1);
+      const int blk = WF == kFp8 ? kTileBytesFp8 : WF == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
+      rs[i] = make_rsrc(a.w[m]);
+      toff[i] = tile * a.C * blk;
+      coff[i] = (a.N[m] / 16) * a.C * kValueBytesFp4 + tile * a.C * kCodeBytesFp4;
       tab[i] = tabs[m];
     }
 
-    f32x4 acc[kTiles][G];
+    f32x4 acc2[2][T][G];
 #pragma unroll
-    for (int i = 0; i < kTiles; ++i)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int g = 0; g < G; ++g) acc[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < T; ++i)
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc2[h][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    int c = c0 + wave;
-    if (c < c1) {
-      WRegs<WF> cur;
-      load_w<WF>(cur, tb, cb, c, lane);
-      for (; c < c1; c += kWaves) {
-        WRegs<WF> nxt;
-        const bool more = c + kWaves < c1;
-        if (more) load_w<WF>(nxt, tb, cb, c + kWaves, lane);
-        XRegs<G> X;
-        load_x<G>(X, xrow, c);
-        compute<WF, F16, G>(cur, X, acc, tab);
-        if (more) cur = nxt;
-      }
-    }
-
-    // Waves' sums into LDS in wave order: red[16i + 4t + v][16g + r].
-#pragma unroll 1
-    for (int w = 0; w < kWaves; ++w) {
-      if (wave == w) {
+    {
+      // Every ring load is issued unconditionally (the wait counts then hold on every path); a chunk past the
+      // segment's end is turned into an out-of-range buffer load (offset >= num_records), which returns zeros
+      // and touches no memory. The chunk count is padded to a multiple of PF; only compute is skipped.
+      WRegs<WF, T> wr[PF];
+      u32x4 xr[PF][G];
+      auto load_stage = [&](int j, int c) {
+        const unsigned oob = c < c1 ? 0u : 0x80000000u;
+        // scheduling barriers keep the issue order (activations, then weights, chunk after chunk) that the
+        // in-order wait counts rely on
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < kTiles; ++i)
+        for (int i = 0; i < G; ++i)
+          xr[j][i] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i] | oob), c * 256, 0));
+        __builtin_amdgcn_sched_barrier(0);
+        load_w<WF, T>(wr[j], rs, toff, coff, c, static_cast<int>(lane_off | oob), slot, oob);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      auto put_x = [&](int j, int sl) {
 #pragma unroll
-          for (int g = 0; g < G; ++g)
+        for (int i = 0; i < G; ++i) *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
+      };
+      const int npad = (c1 - c0 + PF - 1) / PF * PF;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-              float& d = red[16 * i + 4 * t + v][16 * g + r];
-              d = (w == 0) ? acc[i][g][v] : d + acc[i][g][v];
+      for (int j = 0; j < PF - 1; ++j) load_stage(j, c0 + j);
+      if constexpr (BPRE) {
+        u32x4 bc[4][G], bn[4][G];
+        put_x(0, 0);
+        __syncthreads();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) read_b<G>(bc[s], xs[0], s, r, t);
+        for (int base = 0; base < npad; base += PF) {
+#pragma unroll
+          for (int j = 0; j < PF; ++j) {
+            const int it = base + j, c = c0 + it;
+            const int sl = (it + 1) % NSLOT;
+            put_x((j + 1) % PF, sl);
+            __syncthreads();
+            load_stage((j + PF - 1) % PF, c + PF - 1);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
+            if (c < c1) {
+#pragma unroll
+              for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
             }
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+              for (int g = 0; g < G; ++g) bc[s][g] = bn[s][g];
+          }
+        }
+      } else {
+        for (int base = 0; base < npad; base += PF) {
+#pragma unroll
+          for (int j = 0; j < PF; ++j) {
+            const int it = base + j, c = c0 + it;
+            put_x(j, it & 1);
+            __syncthreads();
+            load_stage((j + PF - 1) % PF, c + PF - 1);
+            if (c < c1) compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
+          }
+        }
       }
-      __syncthreads();
     }
+    f32x4 acc[T][G];
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g) acc[i][g] = acc2[0][i][g] + acc2[1][i][g];
 
-    const int out_rows = PAIR ? ROWS / 2 : ROWS;
     if (c0 == 0 && c1 == a.C) {
-      for (int e = threadIdx.x; e < out_rows * a.M; e += kThreads)
-        epilogue_store<PAIR, OUTF32, G>(a, mi, tile0, red, e % out_rows, e / out_rows);
+      epilogue<G, PAIR, OUTF32>(a, mi, wtile0, acc, r, t);
       __syncthreads();
       continue;
     }
 
-    // Split tile group: publish this workgroup's partial, count arrivals; the last one adds all partials
-    // in workgroup order and applies the epilogue.
+    // Split tile group: publish this workgroup's partial (float e of thread tid at [e][tid]), count arrivals;
+    // the last workgroup adds all partials in workgroup order and applies the epilogue. The exchange uses
+    // agent-coherent accesses instead of fences: the partials are stored and loaded with agent-scope relaxed
+    // atomics (write-through past the XCD's L2, and reads that do not hit a stale L2 line), each thread waits
+    // for its stores to complete before the barrier, and only then does thread 0 count the arrival. No
+    // L2-wide writeback or invalidate is needed.
     const int pf = wg_of_unit(static_cast<long long>(tg) * a.C, a.P, a.U);
     const int pl = wg_of_unit(static_cast<long long>(tg) * a.C + a.C - 1, a.P, a.U);
-    constexpr int SLOT = ROWS * COLS;
-    float* slot = a.partials + static_cast<size_t>(2 * p + (tg == tg_first ? 0 : 1)) * SLOT;
-    for (int e = threadIdx.x; e < SLOT; e += kThreads) slot[e] = red[e / COLS][e % COLS];
-    __threadfence();
+    constexpr int SLOT = NACC * kThreads;
+    float* slotp = a.partials + static_cast<size_t>(2 * p + (tg == tg_first ? 0 : 1)) * SLOT + threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+        if (16 * g + r < a.M)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            __hip_atomic_store(slotp + ((i * G + g) * 4 + v) * kThreads, acc[i][g][v], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
-      const int old = atomicAdd(a.counters + tg, 1);
+      const int old = __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last_flag = old == pl - pf;
-      if (last_flag) atomicExch(a.counters + tg, 0);
+      if (last_flag) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (last_flag) {
-      __threadfence();
-      for (int e = threadIdx.x; e < SLOT; e += kThreads) {
-        float s = 0.f;
-        for (int q = pf; q <= pl; ++q) {
-          const int qf = static_cast<int>(unit_start(q, a.P, a.U) / a.C);
-          const float* sq = a.partials + static_cast<size_t>(2 * q + (tg == qf ? 0 : 1)) * SLOT;
-          const float v = __builtin_nontemporal_load(sq + e);
-          s = (q == pf) ? v : s + v;
+      // partials in workgroup order; QB of them in flight at a time (loads may complete in any order, the adds
+      // are in order)
+      constexpr int QB = NACC <= 8 ? 8 : NACC <= 16 ? 4 : 2;
+      for (int q0 = pf; q0 <= pl; q0 += QB) {
+        float pv[QB][NACC];
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+          const int q = q0 + b;
+          if (q <= pl) {
+            const int qf = static_cast<int>(unit_start(q, a.P, a.U) / a.C);
+            const float* sq = a.partials + static_cast<size_t>(2 * q + (tg == qf ? 0 : 1)) * SLOT + threadIdx.x;
+#pragma unroll
+            for (int e = 0; e < NACC; ++e)
+              pv[b][e] = (16 * ((e >> 2) % G) + r < a.M)
+                             ? __hip_atomic_load(sq + e * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                             : 0.f;
+          }
         }
-        red[e / COLS][e % COLS] = s;
+#pragma unroll
+        for (int b = 0; b < QB; ++b) {
+          const int q = q0 + b;
+          if (q <= pl) {
+#pragma unroll
+            for (int i = 0; i < T; ++i)
+#pragma unroll
+              for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                  const float x = pv[b][(i * G + g) * 4 + v];
+                  acc[i][g][v] = (q == pf) ? x : acc[i][g][v] + x;
+                }
+          }
+        }
       }
-      __syncthreads();
-      for (int e = threadIdx.x; e < out_rows * a.M; e += kThreads)
-        epilogue_store<PAIR, OUTF32, G>(a, mi, tile0, red, e % out_rows, e / out_rows);
+      epilogue<G, PAIR, OUTF32>(a, mi, wtile0, acc, r, t);
     }
     __syncthreads();
   }
@@ -361,12 +507,13 @@ struct Mat {
   int ldy;
 };
 
-// Workgroups per launch: about two per CU, a multiple of 8 (one share per XCD), never more than the units.
+// Workgroups per launch: one per CU (a workgroup's four waves fill its SIMDs), a multiple of 8 (one share per
+// XCD), never more than the units.
 // Depends only on the unit count and the device, never on M (row invariance).
 int choose_wgs(long long U) {
   int dev = 0;
   (void)hipGetDevice(&dev);
-  long long P = static_cast<long long>(device_cus(dev)) * 2;
+  long long P = static_cast<long long>(device_cus(dev));
   if (P > U) P = U;
   if (P >= 8) P -= P % 8;
   return static_cast<int>(std::max<long long>(P, 1));
@@ -421,11 +568,11 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     a.N[i] = m.N;
     a.ldy[i] = m.ldy;
     a.tg0[i] = tg;
-    if (!pair) tg += cdiv(m.N / 16, kTiles);
+    if (!pair) tg += cdiv(m.N, kGroupRows);
   }
   if (pair) {
     if (n != 2 || mats[0].N != mats[1].N) return fail(LQ_ERR_SHAPE, nm + ": gate and up must have the same N");
-    tg = cdiv(mats[0].N / 16, kTiles / 2);
+    tg = cdiv(mats[0].N, kGroupRows);
   }
   a.tg0[n] = tg;
   a.TG = tg;
@@ -433,7 +580,7 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   a.P = choose_wgs(a.U);
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  const size_t slot_floats = static_cast<size_t>(kTiles * 16) * (cdiv(M, 16) * 16);
+  const size_t slot_floats = static_cast<size_t>(2) * cdiv(M, 16) * 4 * kThreads;
   int rc = ws->reserve_stream(static_cast<size_t>(2) * a.P * slot_floats * sizeof(float), static_cast<size_t>(tg));
   if (rc) return rc;
   a.partials = ws->partials;
