@@ -117,6 +117,17 @@ int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const 
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
                          int N, int K, void* stream);
 
+/* ---------------- prefill, block-scaled FP8 (additive; reference src/core/kernels.cuh:190-221) ---------------- */
+/* BF16 x [M][K] -> FP8 E4M3 q [M][K] with one FP32 scale per 1x128 group, scale [M][K/128] = amax / 448 (1 for an
+ * all-zero group), q = E4M3_rne(x / scale). The block-scaled counterpart of quant_act_fp8 (kernels.cuh:199). */
+int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* scale, void* stream);
+/* y[M][0..N) (rows ldy apart, BF16) = bf16(sum over 128-value K blocks kb of (xq . W^T over kb) * xs[m][kb] *
+ * ws[n/128][kb]); xq FP8 [M][K], xs FP32 [M][K/128], W tiled FP8 (the stream GEMMs' blob), ws FP32 [N/128][K/128].
+ * N % 128 == 0, K % 128 == 0; M < 1 does nothing. The block-scaled, BF16-out form of prefill_gemm_fp8
+ * (kernels.cuh:213-214) and prefill_gemm_fp8_bf16out (kernels.cuh:239-240). */
+int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws, uint16_t* y,
+                         int ldy, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

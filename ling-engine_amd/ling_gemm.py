@@ -41,6 +41,8 @@ SIGNATURES = {
     "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_residual": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
+    "lq_quant_act_fp8_g128": (_I, [_P, _I, _I, _P, _P, _P]),
+    "lq_prefill_fp8_block": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
 }
 
 
