@@ -12,13 +12,15 @@
 //    block). Any permutation of K inside the block is harmless, since A and B use the same one.
 //  * Weights are the A operand (rows n) and activations the B operand (columns m): a lane's four outputs
 //    share one token and one 128-row weight block, so its block scale is one multiply per token tile.
-//  * A workgroup (4 waves, 2 x 2) computes 128 weight rows x 128 tokens; each wave 64 x 64 (4 x 4 MFMA
-//    tiles). Each K block's operands (16 KB of weights, 16 KB of activations) are staged in LDS (double
-//    buffered) as [row][8 x 16-byte units] with the unit index XOR-swizzled by row, so the fragment reads
-//    are bank-conflict free; the next block's global loads are in flight while the current one computes.
-//  * Tile order: workgroup ids are mapped so that each XCD works through a contiguous band of weight
-//    columns, all token tiles of one weight tile in a row, so a weight block is fetched from HBM once and
-//    reused from that XCD's L2 by every token tile.
+//  * A workgroup (8 waves, 2 per SIMD: 2 along the weights x 4 along the tokens) computes 128 weight rows x
+//    256 tokens; each wave 64 x 64 (4 x 4 MFMA tiles). Each K block's operands (16 KB of weights, 32 KB of
+//    activations) are staged in LDS (double buffered) as [row][8 x 16-byte units] with the unit index
+//    XOR-swizzled by row, so the fragment reads are bank-conflict free. Global loads run two K blocks ahead
+//    through two register staging sets: a block's loads are issued two iterations before it is written to
+//    LDS and computed.
+//  * Tile order: each XCD works through a contiguous range of a grouped raster (8 weight tiles x every
+//    token tile per group), so the workgroups running at once on an XCD share the K slices of both operands
+//    in its L2 instead of re-streaming the whole activation matrix per weight tile.
 #include "lq_common.hpp"
 
 #include <algorithm>
@@ -28,10 +30,11 @@ namespace lq {
 namespace {
 
 constexpr int kBN = 128;  // weight rows per workgroup
-constexpr int kBM = 128;  // tokens per workgroup
-constexpr int kThreads = 256;
+constexpr int kBM = 256;  // tokens per workgroup
+constexpr int kThreads = 512;
+constexpr int kGroupN = 8;  // weight tiles per raster group
 constexpr int kRowBytes = 128;                       // one K block of one row (FP8)
-constexpr int kStage = (kBN + kBM) * kRowBytes;      // 32 KB: weights then activations
+constexpr int kStage = (kBN + kBM) * kRowBytes;      // 48 KB: weights then activations
 
 // Byte offset of 16-byte unit u of row `row` in an LDS operand tile.
 __device__ __forceinline__ int lds_off(int row, int u) { return row * kRowBytes + ((u ^ ((row >> 1) & 7)) << 4); }
@@ -50,56 +53,76 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, t = lane >> 4;
-  const int wn = wave & 1, wm = wave >> 1;  // wave's 64-row weight half and 64-token half
+  const int wn = wave & 1, wm = wave >> 1;  // wave's 64-row weight half and 64-token quarter
 
-  // XCD-banded tile order: hardware places block b on XCD b % 8; logical tile index = xcd band + local.
+  // Tile order. The hardware places block b on XCD b % 8; each XCD takes a contiguous range of the logical
+  // tile order, in which tiles come in groups of kGroupN weight tiles x all token tiles, token tile slowest
+  // within a group. The ~32 workgroups an XCD runs at once then cover kGroupN weight tiles x a few token
+  // tiles, so the K slices of both operands they read at a time are shared in that XCD's L2.
   const int nb = gridDim.x, b = blockIdx.x;
   int tile = b;
   if ((nb & 7) == 0) tile = (b & 7) * (nb >> 3) + (b >> 3);
-  const int tn = tile / a.tiles_m, tm = tile % a.tiles_m;  // weight tile (slow), token tile (fast)
+  const int grp = tile / (kGroupN * a.tiles_m), rem = tile % (kGroupN * a.tiles_m);
+  const int gsize = min(kGroupN, a.tiles_n - grp * kGroupN);
+  const int tn = grp * kGroupN + rem % gsize, tm = rem / gsize;
   const int n0 = tn * kBN, m0 = tm * kBM;
 
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.xq), 0, 0x7fffffff, 0x00020000);
 
-  // Global -> LDS copy plan, 4 + 4 16-byte pieces per thread and K block.
+  // Global -> LDS copy plan, 2 + 4 16-byte pieces per thread and K block.
   // Weights: piece j (0..1023) = tiled block (16-row tile tw = j / 128, piece p = j % 128) of the current chunk;
   // p = ((h*2 + q)*8 + g)*4 + tt holds row g + 8h, values [32 tt + 16 q, +16): LDS row 16 tw + g + 8h, unit 2 tt + q.
-  int wsrc[4], wdst[4], xsrc[4], xdst[4];
+  constexpr int WP = kBN * kRowBytes / 16 / kThreads, XP = kBM * kRowBytes / 16 / kThreads;
+  int wsrc[WP], wdst[WP], xsrc[XP], xdst[XP];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < WP; ++i) {
     const int j = i * kThreads + threadIdx.x;
     const int tw = j >> 7, p = j & 127;
     const int tt = p & 3, g = (p >> 2) & 7, q = (p >> 5) & 1, h = p >> 6;
     wsrc[i] = ((n0 >> 4) + tw) * a.KB * kTileBytesFp8 + p * 16;
     wdst[i] = lds_off(16 * tw + g + 8 * h, 2 * tt + q);
+  }
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
     // activations: row j / 8 of the token tile, unit j % 8 (rows past M read as zeros, out of range)
+    const int j = i * kThreads + threadIdx.x;
     const int row = j >> 3, u = j & 7, m = m0 + row;
     xsrc[i] = m < a.M ? m * a.K + u * 16 : static_cast<int>(0x80000000u);
     xdst[i] = kBN * kRowBytes + lds_off(row, u);
   }
 
-  u32x4 stg[8];
-  auto load = [&](int kb) {
+  // per-lane block-scale inputs: this lane's four tokens (one per token tile); their activation scales travel
+  // with the block's operands (loaded into the same staging set), so waiting for a scale never waits for a
+  // later block's prefetch (loads retire in issue order)
+  int xso[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      stg[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, wsrc[i], kb * kTileBytesFp8, 0));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      stg[4 + i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, xsrc[i], kb * kRowBytes, 0));
-  };
-  auto store = [&](uint8_t* st) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(st + wdst[i]) = stg[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(st + xdst[i]) = stg[4 + i];
-  };
-
-  // per-lane block-scale inputs: this lane's four tokens (one per token tile)
-  int mt[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) mt[j] = min(m0 + wm * 64 + 16 * j + r, a.M - 1);
+  for (int j = 0; j < 4; ++j) xso[j] = min(m0 + wm * 64 + 16 * j + r, a.M - 1) * a.KB * 4;
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xs), 0, 0x7fffffff, 0x00020000);
   const float* wsrow = a.ws + static_cast<size_t>(tn) * a.KB;
+
+  u32x4 stg[2][WP + XP];
+  float xsc[2][4];
+  auto load = [&](int sset, int kb) {
+    const unsigned oob = kb < a.KB ? 0u : 0x80000000u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xsc[sset][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, static_cast<int>(xso[j] | oob), kb * 4, 0));
+#pragma unroll
+    for (int i = 0; i < WP; ++i)
+      stg[sset][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, static_cast<int>(wsrc[i] | oob), kb * kTileBytesFp8, 0));
+#pragma unroll
+    for (int i = 0; i < XP; ++i)
+      stg[sset][WP + i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, static_cast<int>(xsrc[i] | oob), kb * kRowBytes, 0));
+  };
+  auto store = [&](int sset, uint8_t* st) {
+#pragma unroll
+    for (int i = 0; i < WP; ++i) *reinterpret_cast<u32x4*>(st + wdst[i]) = stg[sset][i];
+#pragma unroll
+    for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4*>(st + xdst[i]) = stg[sset][WP + i];
+  };
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -107,47 +130,53 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  load(0);
-  store(smem);
-  __syncthreads();
-  for (int kb = 0; kb < a.KB; ++kb) {
-    const uint8_t* st = smem + (kb & 1) * kStage;
-    if (kb + 1 < a.KB) load(kb + 1);
-    // fragments: weights rows wn*64 + 16i + r, activations rows wm*64 + 16j + r; 32 bytes at K 32t
-    i32x8 af[4], bf[4];
+  // K block kb: loaded into staging set kb % 2 two iterations ahead, written to LDS buffer kb % 2, computed.
+  // LDS buffer kb % 2 was last read by block kb - 2, which every wave finished before the barrier of kb - 1.
+  load(0, 0);
+  load(1, 1);
+  const int KBP = (a.KB + 1) & ~1;
+  for (int kb0 = 0; kb0 < KBP; kb0 += 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wn * 64 + 16 * i + r;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t + 1));
-      af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
+    for (int ph = 0; ph < 2; ++ph) {
+      const int kb = kb0 + ph;
+      uint8_t* st = smem + ph * kStage;
+      store(ph, st);
+      // the block's combined scales, taken before this staging set is refilled
+      const float wsc = kb < a.KB ? wsrow[kb] : 0.f;
+      float sc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wm * 64 + 16 * j + r;
-      const uint8_t* xb = st + kBN * kRowBytes;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t));
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t + 1));
-      bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-    const float wsc = wsrow[kb];
-    float sc[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) sc[j] = a.xs[static_cast<size_t>(mt[j]) * a.KB + kb] * wsc;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
-        const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0,
-                                                                        127, 0, 127);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc[j], acc[i][j][v]);
-      }
-    if (kb + 1 < a.KB) {
-      __syncthreads();  // everyone is done reading the other buffer's previous block
-      store(smem + ((kb + 1) & 1) * kStage);
+      for (int j = 0; j < 4; ++j) sc[j] = xsc[ph][j] * wsc;
       __syncthreads();
+      load(ph, kb + 2);  // out-of-range blocks load nothing
+      if (kb < a.KB) {
+        // fragments: weights rows wn*64 + 16i + r, activations rows wm*64 + 16j + r; 32 bytes at K 32t
+        i32x8 af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = wn * 64 + 16 * i + r;
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t));
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t + 1));
+          af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int row = wm * 64 + 16 * j + r;
+          const uint8_t* xb = st + kBN * kRowBytes;
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t));
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t + 1));
+          bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
+            const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf[j], f32x4{0.f, 0.f, 0.f, 0.f},
+                                                                            0, 0, 0, 127, 0, 127);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc[j], acc[i][j][v]);
+          }
+      }
     }
   }
 
@@ -226,6 +255,11 @@ int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_
   a.tiles_m = cdiv(M, kBM);
   a.tiles_n = N / kBN;
   const long long blocks = static_cast<long long>(a.tiles_m) * a.tiles_n;
+  // 96 KB of dynamic LDS is above the default per-launch limit; raise it (idempotent, per process).
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_fp8_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                          2 * kStage);
+  if (attr != hipSuccess) return fail(LQ_ERR_LAUNCH, std::string("prefill_gemm: ") + hipGetErrorString(attr));
   hipLaunchKernelGGL(prefill_fp8_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 2 * kStage,
                      static_cast<hipStream_t>(stream), a);
   return check_launch("prefill_gemm");
