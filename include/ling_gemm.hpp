@@ -1,0 +1,109 @@
+// ling_gemm.hpp: the C++ face of libling_gemm.so, shaped like ling-engine's `ling::kernels` quantized GEMM
+// functions (reference src/core/kernels.cuh:162-295) so an engine written against them recompiles with HIP.
+// Each function forwards to the C ABI (ling_gemm.h) and throws std::runtime_error with the library's message
+// on failure; the messages follow the reference's texts ("stream_gemm: K must be a multiple of 128", ...).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+
+#include "ling_gemm.h"
+
+namespace ling::kernels {
+
+inline void lq_check(int rc) {
+  if (rc != LQ_OK) throw std::runtime_error(lq_last_error());
+}
+
+constexpr int kMaxStreamRows = LQ_MAX_STREAM_ROWS;
+constexpr int kScaleCodes = 64;
+
+// kernels.cuh:281-287
+struct StreamTarget {
+  const uint8_t* w;
+  const uint8_t* wscale;  // NVFP4: a coded blob's scale-code table; nullptr for a raw blob and for FP8
+  float scale;            // NVFP4 global scale, or the FP8 per-tensor scale
+  float* y;
+  int N;
+};
+
+// ---- tiled layout (kernels.cuh:162-188) ----
+inline size_t tiled_bytes_nvfp4(int N, int K) { return lq_tiled_bytes_nvfp4(N, K); }
+inline size_t tiled_bytes_fp8(int N, int K) { return lq_tiled_bytes_fp8(N, K); }
+inline size_t tiled_bytes_nvfp4_coded(int N, int K) { return lq_tiled_bytes_nvfp4_coded(N, K); }
+inline void retile_nvfp4(const uint8_t* w, const uint8_t* wscale, uint8_t* out, int N, int K, hipStream_t s) {
+  lq_check(lq_retile_nvfp4(w, wscale, out, N, K, s));
+}
+inline void retile_fp8(const uint8_t* w, uint8_t* out, int N, int K, hipStream_t s) {
+  lq_check(lq_retile_fp8(w, out, N, K, s));
+}
+inline bool scale_code_table(const uint8_t* scales, size_t n, uint8_t (&table)[kScaleCodes], uint8_t (&code_of)[256]) {
+  return lq_scale_code_table(scales, n, table, code_of) == 1;
+}
+inline void retile_nvfp4_coded(const uint8_t* w, const uint8_t* wscale, const uint8_t* code_of_dev, uint8_t* out,
+                               uint8_t* raw_scales, int N, int K, hipStream_t s) {
+  lq_check(lq_retile_nvfp4_coded(w, wscale, code_of_dev, out, raw_scales, N, K, s));
+}
+inline void dequant_tiled_nvfp4(const uint8_t* tw, float scale2, uint16_t* out_bf16, int N, int K, hipStream_t s,
+                                const uint8_t* raw_scales = nullptr) {
+  lq_check(lq_dequant_tiled_nvfp4(tw, scale2, out_bf16, N, K, s, raw_scales));
+}
+inline void dequant_tiled_fp8(const uint8_t* tw, float wscale, uint16_t* out_bf16, int N, int K, hipStream_t s) {
+  lq_check(lq_dequant_tiled_fp8(tw, wscale, out_bf16, N, K, s));
+}
+
+// ---- rows path (kernels.cuh:266-295) ----
+inline void to_half_rows(const float* x, int M, int K, __half* out, float* xinv, hipStream_t s) {
+  lq_check(lq_to_half_rows(x, M, K, reinterpret_cast<uint16_t*>(out), xinv, s));
+}
+inline void bf16_to_half_rows(const uint16_t* x_bf16, int M, int K, __half* out, float* xinv, hipStream_t s) {
+  lq_check(lq_bf16_to_half_rows(x_bf16, M, K, reinterpret_cast<uint16_t*>(out), xinv, s));
+}
+inline void stream_gemm_nvfp4(const __half* x, const float* xinv, int M, const uint8_t* w, const uint8_t* wscale,
+                              float scale2, float* y, int N, int K, hipStream_t s) {
+  lq_check(lq_stream_gemm_nvfp4(reinterpret_cast<const uint16_t*>(x), xinv, M, w, wscale, scale2, y, N, K, s));
+}
+inline void stream_gemm_fp8(const __half* x, const float* xinv, int M, const uint8_t* w, float wscale, float* y, int N,
+                            int K, hipStream_t s) {
+  lq_check(lq_stream_gemm_fp8(reinterpret_cast<const uint16_t*>(x), xinv, M, w, wscale, y, N, K, s));
+}
+inline void stream_gemm_multi(bool nvfp4, const __half* x, const float* xinv, int M, const StreamTarget* t, int n, int K,
+                              hipStream_t s) {
+  lq_stream_target c[4];
+  if (n < 1 || n > 4 || !t) throw std::runtime_error("stream_gemm: 1 to 4 matrices per launch");
+  for (int i = 0; i < n; ++i) c[i] = lq_stream_target{t[i].w, t[i].wscale, t[i].scale, t[i].y, t[i].N};
+  lq_check(lq_stream_gemm_multi(nvfp4 ? 1 : 0, reinterpret_cast<const uint16_t*>(x), xinv, M, c, n, K, s));
+}
+
+// ---- rows path, BF16 formats (additive) ----
+inline void stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N, int K,
+                          hipStream_t s) {
+  lq_check(lq_stream_fp8_pc(x, M, w, wscale_n, y, N, K, s));
+}
+inline void stream_fp8_pc_silu_mul(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate,
+                                   const uint8_t* w_up, const float* s_up, uint16_t* h, int N, int K, hipStream_t s) {
+  lq_check(lq_stream_fp8_pc_silu_mul(x, M, w_gate, s_gate, w_up, s_up, h, N, K, s));
+}
+inline void stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n,
+                                   const uint16_t* resid, uint16_t* y, int N, int K, hipStream_t s) {
+  lq_check(lq_stream_fp8_pc_residual(x, M, w, wscale_n, resid, y, N, K, s));
+}
+inline void stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2,
+                              uint16_t* y, int N, int K, hipStream_t s) {
+  lq_check(lq_stream_nvfp4_bf16(x, M, w, table, scale2, y, N, K, s));
+}
+
+// ---- prefill (block-scaled FP8; kernels.cuh:190-221 for the reference's per-tensor forms) ----
+inline void quant_act_fp8_g128(const uint16_t* x_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t s) {
+  lq_check(lq_quant_act_fp8_g128(x_bf16, M, K, q, scale, s));
+}
+inline void prefill_gemm_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws,
+                                   uint16_t* y_bf16, int ldy, int N, int K, hipStream_t s) {
+  lq_check(lq_prefill_fp8_block(xq, xs, M, w, ws, y_bf16, ldy, N, K, s));
+}
+
+}  // namespace ling::kernels

@@ -64,3 +64,51 @@ def test_errors_are_reported_before_any_launch():
     assert b"1 to 4 matrices per launch" in lib.lq_last_error()
     assert lib.lq_retile_fp8(None, None, 17, 128, None) == 1
     assert b"N % 16 and K % 128 must be 0" in lib.lq_last_error()
+
+
+CPP = r"""
+#include <cstdio>
+#include <cstring>
+#include <stdexcept>
+#include "ling_gemm.hpp"
+namespace K = ling::kernels;
+int main() {
+  int fails = 0;
+  if (K::tiled_bytes_fp8(5120, 5120) != size_t(5120) * 5120) ++fails;
+  if (K::tiled_bytes_nvfp4(16, 128) != 16 * 64 + 16 * 8) ++fails;
+  uint8_t scales[4] = {0x38, 0x40, 0x38, 0x41}, table[64], code_of[256];
+  if (!K::scale_code_table(scales, 4, table, code_of) || table[0] != 0x38 || code_of[0x41] != 2) ++fails;
+  // the reference's error texts, thrown before any device work
+  const char* want[] = {"stream_gemm: K must be a multiple of 128", "stream_gemm: M must be in [1, 80]",
+                        "stream_gemm: 1 to 4 matrices per launch", "retile_fp8: N % 16 and K % 128 must be 0",
+                        "prefill_gemm: N % 128 and K % 128 must be 0"};
+  for (int c = 0; c < 5; ++c) {
+    try {
+      if (c == 0) K::stream_gemm_fp8(nullptr, nullptr, 1, nullptr, 1.f, nullptr, 16, 100, nullptr);
+      if (c == 1) K::stream_gemm_fp8(nullptr, nullptr, 81, nullptr, 1.f, nullptr, 16, 128, nullptr);
+      if (c == 2) K::stream_gemm_multi(false, nullptr, nullptr, 1, nullptr, 5, 128, nullptr);
+      if (c == 3) K::retile_fp8(nullptr, nullptr, 17, 128, nullptr);
+      if (c == 4) K::prefill_gemm_fp8_block(nullptr, nullptr, 4, nullptr, nullptr, nullptr, 64, 64, 128, nullptr);
+      ++fails;
+    } catch (const std::runtime_error& e) {
+      if (std::strcmp(e.what(), want[c]) != 0) { std::printf("got '%s'\n", e.what()); ++fails; }
+    }
+  }
+  std::printf("fails=%d\n", fails);
+  return fails;
+}
+"""
+
+
+def test_cpp_wrapper_compiles_and_throws_reference_messages(tmp_path):
+    import subprocess
+    src = tmp_path / "w.cpp"
+    src.write_text(CPP)
+    exe = tmp_path / "w"
+    libdir = os.path.dirname(LIB)
+    cmd = ["/opt/rocm/bin/hipcc", "-std=c++17", "-O1", str(src), "-o", str(exe), f"-I{ROOT}/include", f"-L{libdir}",
+           "-lling_gemm", f"-Wl,-rpath,{libdir}", "--offload-arch=gfx950"]
+    subprocess.run(cmd, check=True, capture_output=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "fails=0" in r.stdout
