@@ -63,7 +63,7 @@ struct StreamArgs {
   const float* xinv;  // [M] row scales of an FP16 copy, or null
   int M, K, C;        // C = K / 128
   int P;              // logical workgroups
-  long long U;        // units = TG * C
+  int U;              // units = TG * C (U * (P + 1) < 2^31: the unit arithmetic is 32-bit)
   int TG;             // tile groups
   int count;          // matrices
   const uint8_t* w[kMaxMats];
@@ -178,12 +178,56 @@ __device__ __forceinline__ void compute_lds(const WRegs<WF, T>& R, const uint8_t
   }
 }
 
-__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU v / (1 + e^-v), with the hardware reciprocal (1 ulp) in place of the division.
+__device__ __forceinline__ float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
+// What the epilogue reads besides the sums, for one lane: the output scales of its 4 channels per tile
+// (per-channel vector, or the matrix's scalar), the residual's 4 values per tile and token group, and the
+// row scales. Loaded in one batch of vector loads (for the range's first and last tile groups at kernel
+// start), so finishing a tile group waits on no memory read.
+template <int G, int T>
+struct EpiIn {
+  f32x4 sv[T];
+  u32x2 rr[T][G];
+  float xi[G];
+};
+
+// Tile i's first output row for this lane: PAIR = gate tiles then the same up tiles.
+template <bool PAIR, int T>
+__device__ __forceinline__ int epi_row(int wtile0, int i, int t) {
+  return (wtile0 + (PAIR ? i % (T / 2) : i)) * 16 + 4 * t;
+}
+
+template <int G, bool PAIR, bool OUTF32, int T = tiles_per_wave<PAIR>()>
+__device__ __forceinline__ void epi_load(const StreamArgs& a, int mi, int wtile0, EpiIn<G, T>& e, int r, int t) {
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
+    const int n = epi_row<PAIR, T>(wtile0, i, t);
+    const float sc = a.sc[m];
+    e.sv[i] = f32x4{sc, sc, sc, sc};
+    if (a.svec[m] && n < a.N[m]) e.sv[i] = *reinterpret_cast<const f32x4*>(a.svec[m] + n);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int tok = 16 * g + r;
+      e.rr[i][g] = u32x2{0u, 0u};
+      if constexpr (!PAIR && !OUTF32) {
+        if (a.resid[m] && tok < a.M && n < a.N[m])
+          e.rr[i][g] = *reinterpret_cast<const u32x2*>(a.resid[m] + static_cast<size_t>(tok) * a.ldy[m] + n);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int tok = 16 * g + r;
+    e.xi[g] = (a.xinv && tok < a.M) ? a.xinv[tok] : 1.0f;
+  }
+}
 
 // Epilogue of one lane's outputs: acc[i][g][v] is row 16 * tile(i) + 4t + v, token 16g + r.
 template <int G, bool PAIR, bool OUTF32, int T = tiles_per_wave<PAIR>()>
-__device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0, const f32x4 (&acc)[T][G], int r,
-                                         int t) {
+__device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0, const f32x4 (&acc)[T][G],
+                                         const EpiIn<G, T>& e, int r, int t) {
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int tok = 16 * g + r;
@@ -191,36 +235,35 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
     if constexpr (PAIR) {
 #pragma unroll
       for (int i = 0; i < T / 2; ++i) {
-        const int n = (wtile0 + i) * 16 + 4 * t;
+        const int n = epi_row<PAIR, T>(wtile0, i, t);
         if (n >= a.N[0]) continue;
         uint16_t o[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          const float gs = acc[i][g][v] * (a.svec[0] ? a.svec[0][n + v] : a.sc[0]);
-          const float us = acc[i + T / 2][g][v] * (a.svec[1] ? a.svec[1][n + v] : a.sc[1]);
+          const float gs = acc[i][g][v] * e.sv[i][v];
+          const float us = acc[i + T / 2][g][v] * e.sv[i + T / 2][v];
           o[v] = f32_to_bf16(silu(gs) * us);
         }
         uint16_t* dst = reinterpret_cast<uint16_t*>(a.y[0]) + static_cast<size_t>(tok) * a.ldy[0] + n;
         *reinterpret_cast<u32x2*>(dst) = u32x2{o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16)};
       }
     } else {
-      const float xi = a.xinv ? a.xinv[tok] : 1.0f;
 #pragma unroll
       for (int i = 0; i < T; ++i) {
-        const int n = (wtile0 + i) * 16 + 4 * t;
+        const int n = epi_row<PAIR, T>(wtile0, i, t);
         if (n >= a.N[mi]) continue;
         float vv[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-          vv[v] = acc[i][g][v] * (a.svec[mi] ? a.svec[mi][n + v] : a.sc[mi]);
-          if (a.xinv) vv[v] = vv[v] * xi;
+          vv[v] = acc[i][g][v] * e.sv[i][v];
+          if (a.xinv) vv[v] = vv[v] * e.xi[g];
         }
         const size_t o = static_cast<size_t>(tok) * a.ldy[mi] + n;
         if constexpr (OUTF32) {
           *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.y[mi]) + o) = f32x4{vv[0], vv[1], vv[2], vv[3]};
         } else {
           if (a.resid[mi]) {
-            const u32x2 rr = *reinterpret_cast<const u32x2*>(a.resid[mi] + o);
+            const u32x2 rr = e.rr[i][g];
             vv[0] = vv[0] + bf16_to_f32(rr.x & 0xffff);
             vv[1] = vv[1] + bf16_to_f32(rr.x >> 16);
             vv[2] = vv[2] + bf16_to_f32(rr.y & 0xffff);
@@ -235,10 +278,140 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
   }
 }
 
-__device__ __forceinline__ int wg_of_unit(long long u, int P, long long U) {
-  return static_cast<int>(((u + 1) * P - 1) / U);
+// Workgroup p's units are [unit_start(p), unit_start(p + 1)); wg_of_unit is the workgroup of unit u.
+__device__ __forceinline__ int wg_of_unit(int u, int P, int U) { return ((u + 1) * P - 1) / U; }
+__device__ __forceinline__ int unit_start(int p, int P, int U) { return p * U / P; }
+
+// Tiles of tile group tg that this wave streams: PAIR = gate tile wtile0 then the same up tile; else tiles
+// wtile0 .. of matrix mi.
+template <int WF, int T, bool PAIR>
+struct SegTiles {
+  int mi, wtile0;
+  __amdgpu_buffer_rsrc_t rs[T];
+  int toff[T], coff[T];
+};
+
+template <int WF, int T, bool PAIR>
+__device__ __forceinline__ void seg_tiles(const StreamArgs& a, int tg, int wave, SegTiles<WF, T, PAIR>& s) {
+  int mi = 0;
+  if constexpr (!PAIR) {
+    while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
+  }
+  s.mi = mi;
+  s.wtile0 = (tg - a.tg0[mi]) * (kGroupRows / 16) + wave * (PAIR ? T / 2 : T);
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
+    const int tile = min((PAIR ? s.wtile0 + (i % (T / 2)) : s.wtile0 + i), a.N[m] / 16 - 1);
+    const int blk = WF == kFp8 ? kTileBytesFp8 : WF == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
+    s.rs[i] = make_rsrc(a.w[m]);
+    s.toff[i] = tile * a.C * blk;
+    s.coff[i] = (a.N[m] / 16) * a.C * kValueBytesFp4 + tile * a.C * kCodeBytesFp4;
+  }
 }
-__device__ __forceinline__ long long unit_start(int p, int P, long long U) { return static_cast<long long>(p) * U / P; }
+
+// Partial sums of a split tile group: workgroup q's slot w (0: its range's first tile group, 1: its last)
+// holds thread tid's T x G accumulator vectors at [j = i * G + g][tid], 16 bytes each. They are written and
+// read with agent-coherent (sc1) buffer accesses: stores write through past the XCD's L2 and loads do not
+// hit a stale L2 line, so the exchange needs no cache-wide writeback or invalidate.
+constexpr int kSc1 = 16;  // cache-policy operand: SC1
+
+template <int G, int T>
+__device__ __forceinline__ int slot_off(int q, int which) {
+  return (2 * q + which) * (T * G * 16 * kThreads) + static_cast<int>(threadIdx.x) * 16;
+}
+
+// Where the partials of tile group tg are: workgroups pf .. pl touch it; a workgroup's partial of tg is in
+// its slot 0 when tg is its range's first tile group (every workgroup after pf starts inside tg; pf itself
+// only when its range starts exactly at tg's first chunk), else in slot 1.
+struct SplitInfo {
+  int pf, pl;
+  bool pf_first;
+};
+__device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
+  SplitInfo s;
+  s.pf = wg_of_unit(tg * a.C, a.P, a.U);
+  s.pl = wg_of_unit(tg * a.C + a.C - 1, a.P, a.U);
+  s.pf_first = unit_start(s.pf, a.P, a.U) == tg * a.C;
+  return s;
+}
+
+// The finishing step of split tile groups: the last workgroup to arrive adds every workgroup's partial in
+// workgroup order. Both of the range's tile groups (first, last) are reduced together, QB partials of each
+// in flight at a time: loads may complete in any order, the adds are in order.
+template <int G, int T>
+__device__ __forceinline__ void reduce_partials(const StreamArgs& a, int p, const bool (&doit)[2],
+                                                const SplitInfo (&si)[2], f32x4 (&accF)[T][G], f32x4 (&accL)[T][G],
+                                                int r) {
+  constexpr int NV = T * G;  // accumulator vectors per thread
+  constexpr int QB = NV <= 2 ? 4 : 2;
+  const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
+  const int n[2] = {doit[0] ? si[0].pl - si[0].pf + 1 : 0, doit[1] ? si[1].pl - si[1].pf + 1 : 0};
+  const int nmax = max(n[0], n[1]);
+  // rows past M read nothing (an out-of-range offset returns zeros): they only reach outputs never stored
+  unsigned rowmask[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) rowmask[g] = 16 * g + r < a.M ? 0u : 0x80000000u;
+  f32x4 own[2][T][G];
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      own[0][i][g] = accF[i][g];
+      own[1][i][g] = accL[i][g];
+    }
+  for (int q0 = 0; q0 < nmax; q0 += QB) {
+    // Unconditional loads: a position past a group's count, or this workgroup's own partial (kept in
+    // registers), reads nothing.
+    f32x4 pv[2][QB][NV];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int b = 0; b < QB; ++b) {
+        const int k = q0 + b, q = si[h].pf + k;
+        const unsigned skip = (k < n[h] && q != p) ? 0u : 0x80000000u;
+        const int off = slot_off<G, T>(q, (k > 0 || si[h].pf_first) ? 0 : 1);
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+            pv[h][b][i * G + g] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           prs, static_cast<int>((off + (i * G + g) * 16 * kThreads) | skip | rowmask[g]), 0, kSc1));
+      }
+#pragma unroll
+    for (int b = 0; b < QB; ++b) {
+      const int k = q0 + b;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const bool mine = si[h].pf + k == p;
+#pragma unroll
+        for (int i = 0; i < T; ++i)
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const f32x4 x = mine ? own[h][i][g] : pv[h][b][i * G + g];
+            if (k < n[h]) {
+              f32x4& d = h ? accL[i][g] : accF[i][g];
+              d = k == 0 ? x : d + x;
+            }
+          }
+      }
+    }
+  }
+}
+
+template <int G, int T>
+__device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int which, const f32x4 (&acc)[T][G],
+                                                int r) {
+  const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
+  const int off = slot_off<G, T>(p, which);
+#pragma unroll
+  for (int i = 0; i < T; ++i)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+      if (16 * g + r < a.M)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[i][g], prs, off + (i * G + g) * 16 * kThreads, 0, kSc1);
+}
 
 template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
@@ -249,11 +422,10 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   constexpr bool BPRE = G <= 2;
   constexpr int NSLOT = BPRE ? 3 : 2;
   constexpr int XS_BYTES = 16 * G * 256;  // one chunk of activations, 16G rows
-  constexpr int NACC = T * G * 4;          // accumulator floats per lane
   static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
   __shared__ __attribute__((aligned(16))) uint8_t xs[NSLOT][XS_BYTES];
   __shared__ uint8_t tabs[kMaxMats][64];
-  __shared__ int last_flag;
+  __shared__ int last_flag[2];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, t = lane >> 4;
 
@@ -266,8 +438,11 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   // share an XCD, so a tile group's partials are exchanged within one L2.
   int p = blockIdx.x;
   if ((a.P & 7) == 0) p = (blockIdx.x & 7) * (a.P >> 3) + (blockIdx.x >> 3);
-  const long long u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
-  const int tg_first = static_cast<int>(u0 / a.C);
+  const int u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
+  const int n_it = u1 - u0;  // chunks this workgroup streams
+  if (n_it <= 0) return;
+  const int tg_first = u0 / a.C, tg_last = (u1 - 1) / a.C;
+  const int cfirst = u0 - tg_first * a.C;
 
   // This thread's share of a chunk's activations: units q = i * 256 + tid of the 16G x 16 units (row q / 16,
   // 16-byte unit q % 16). Rows past M read as zeros from out-of-range offsets (their MFMA columns are never
@@ -284,187 +459,187 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   const int slot = r * 4 + t;
   const int lane_off = WF == kFp8 ? (((r >> 3) * 16 + (r & 7)) * 4 + t) * 16 : slot * 16;
 
-  // The range's segments (one per tile group it touches), the split ones first: a split tile group's other
-  // workgroups also process their share of it first, so its reduction happens early, not at the kernel's end.
-  const int nseg = u1 > u0 ? static_cast<int>((u1 - 1) / a.C) - tg_first + 1 : 0;
-  const bool tail_split = nseg > 1 && (u1 % a.C) != 0;
-  for (int k = 0; k < nseg; ++k) {
-    const int sidx = tail_split ? (k == 0 ? nseg - 1 : k - 1) : k;
-    const int tg = tg_first + sidx;
-    const int c0 = sidx == 0 ? static_cast<int>(u0 % a.C) : 0;
-    const int c1 = static_cast<int>(min(static_cast<long long>(a.C), u1 - static_cast<long long>(tg) * a.C));
+  // The workgroup's units form one continuous stream through the register ring, across tile-group
+  // boundaries: the load cursor (ltg, lc) runs PF - 1 chunks ahead of the compute cursor (ctg, cc).
+  int ltg = tg_first, lc = cfirst, lleft = n_it;
+  SegTiles<WF, T, PAIR> L;
+  seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
+  int ctg = tg_first, cc = cfirst;
+  int cmi = L.mi, cwtile0 = L.wtile0;
 
-    // This wave's tiles: PAIR = gate tile wtile0 then the same up tile; else tile wtile0 of one matrix.
-    int mi = 0;
-    if constexpr (!PAIR) {
-      while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
+  WRegs<WF, T> wr[PF];
+  u32x4 xr[PF][G];
+  // Every ring load is issued unconditionally (the wait counts then hold on every path); a load past the
+  // stream's end is turned into an out-of-range buffer load (offset >= num_records), which returns zeros and
+  // touches no memory.
+  auto load_stage = [&](int j) {
+    const unsigned oob = lleft > 0 ? 0u : 0x80000000u;
+    // scheduling barriers keep the issue order (activations, then weights, chunk after chunk) that the
+    // in-order wait counts rely on
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      xr[j][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i] | oob), lc * 256, 0));
+    __builtin_amdgcn_sched_barrier(0);
+    load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | oob), slot, oob);
+    __builtin_amdgcn_sched_barrier(0);
+    if (lleft > 0) {
+      --lleft;
+      if (++lc == a.C) {
+        lc = 0;
+        ++ltg;
+        if (lleft > 0) seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
+      }
     }
-    const int wtile0 = (tg - a.tg0[mi]) * (kGroupRows / 16) + wave * (PAIR ? T / 2 : T);
-    __amdgpu_buffer_rsrc_t rs[T];
-    int toff[T], coff[T];
-    const uint8_t* tab[T];
+  };
+  auto put_x = [&](int j, int sl) {
 #pragma unroll
-    for (int i = 0; i < T; ++i) {
-      const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
-      const int tile = min((PAIR ? wtile0 + (i % (T / 2)) : wtile0 + i), a.N[m] / 16 - 1);
-      const int blk = WF == kFp8 ? kTileBytesFp8 : WF == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
-      rs[i] = make_rsrc(a.w[m]);
-      toff[i] = tile * a.C * blk;
-      coff[i] = (a.N[m] / 16) * a.C * kValueBytesFp4 + tile * a.C * kCodeBytesFp4;
-      tab[i] = tabs[m];
-    }
+    for (int i = 0; i < G; ++i) *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
+  };
 
-    f32x4 acc2[2][T][G];
+  // Accumulators are split by MFMA step parity; the first tile group's sums wait in accF for the end of the
+  // stream, a tile group wholly inside the range is finished where it ends.
+  f32x4 acc2[2][T][G], accF[T][G];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int i = 0; i < T; ++i)
+    for (int i = 0; i < T; ++i)
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc2[h][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    {
-      // Every ring load is issued unconditionally (the wait counts then hold on every path); a chunk past the
-      // segment's end is turned into an out-of-range buffer load (offset >= num_records), which returns zeros
-      // and touches no memory. The chunk count is padded to a multiple of PF; only compute is skipped.
-      WRegs<WF, T> wr[PF];
-      u32x4 xr[PF][G];
-      auto load_stage = [&](int j, int c) {
-        const unsigned oob = c < c1 ? 0u : 0x80000000u;
-        // scheduling barriers keep the issue order (activations, then weights, chunk after chunk) that the
-        // in-order wait counts rely on
-        __builtin_amdgcn_sched_barrier(0);
+      for (int g = 0; g < G; ++g) acc2[h][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto fold = [&](f32x4 (&out)[T][G]) {
 #pragma unroll
-        for (int i = 0; i < G; ++i)
-          xr[j][i] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i] | oob), c * 256, 0));
-        __builtin_amdgcn_sched_barrier(0);
-        load_w<WF, T>(wr[j], rs, toff, coff, c, static_cast<int>(lane_off | oob), slot, oob);
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      auto put_x = [&](int j, int sl) {
+    for (int i = 0; i < T; ++i)
 #pragma unroll
-        for (int i = 0; i < G; ++i) *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
-      };
-      const int npad = (c1 - c0 + PF - 1) / PF * PF;
-#pragma unroll
-      for (int j = 0; j < PF - 1; ++j) load_stage(j, c0 + j);
-      if constexpr (BPRE) {
-        u32x4 bc[4][G], bn[4][G];
-        put_x(0, 0);
-        __syncthreads();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) read_b<G>(bc[s], xs[0], s, r, t);
-        for (int base = 0; base < npad; base += PF) {
-#pragma unroll
-          for (int j = 0; j < PF; ++j) {
-            const int it = base + j, c = c0 + it;
-            const int sl = (it + 1) % NSLOT;
-            put_x((j + 1) % PF, sl);
-            __syncthreads();
-            load_stage((j + PF - 1) % PF, c + PF - 1);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
-            if (c < c1) {
-#pragma unroll
-              for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-#pragma unroll
-              for (int g = 0; g < G; ++g) bc[s][g] = bn[s][g];
-          }
-        }
+      for (int g = 0; g < G; ++g) {
+        out[i][g] = acc2[0][i][g] + acc2[1][i][g];
+        acc2[0][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        acc2[1][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  auto after_chunk = [&](int it) {
+    if (++cc == a.C && it + 1 < n_it) {
+      if (ctg == tg_first) {
+        fold(accF);
       } else {
-        for (int base = 0; base < npad; base += PF) {
+        f32x4 accM[T][G];
+        fold(accM);
+        EpiIn<G, T> eM;
+        epi_load<G, PAIR, OUTF32>(a, cmi, cwtile0, eM, r, t);
+        epilogue<G, PAIR, OUTF32>(a, cmi, cwtile0, accM, eM, r, t);
+        // Let these stores complete here: with stores of unknown completion order in flight, every later wait
+        // on the ring would have to drain it (vmcnt(0)); after this wait the ring's waits stay partial.
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
+      }
+      ++ctg;
+      cc = 0;
+      SegTiles<WF, T, PAIR> s;
+      seg_tiles<WF, T, PAIR>(a, ctg, wave, s);
+      cmi = s.mi;
+      cwtile0 = s.wtile0;
+    }
+  };
+  auto tables = [&](const uint8_t* (&tab)[T]) {
 #pragma unroll
-          for (int j = 0; j < PF; ++j) {
-            const int it = base + j, c = c0 + it;
-            put_x(j, it & 1);
-            __syncthreads();
-            load_stage((j + PF - 1) % PF, c + PF - 1);
-            if (c < c1) compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
-          }
+    for (int i = 0; i < T; ++i) tab[i] = tabs[PAIR ? (i < T / 2 ? 0 : 1) : cmi];
+  };
+
+  // The epilogue inputs of the range's first and last tile groups, read ahead of the weight stream.
+  SegTiles<WF, T, PAIR> sF, sL;
+  seg_tiles<WF, T, PAIR>(a, tg_first, wave, sF);
+  seg_tiles<WF, T, PAIR>(a, tg_last, wave, sL);
+  EpiIn<G, T> eF, eL;
+  epi_load<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, eF, r, t);
+  epi_load<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, eL, r, t);
+
+  const int npad = (n_it + PF - 1) / PF * PF;
+#pragma unroll
+  for (int j = 0; j < PF - 1; ++j) load_stage(j);
+  if constexpr (BPRE) {
+    u32x4 bc[4][G], bn[4][G];
+    put_x(0, 0);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 4; ++s) read_b<G>(bc[s], xs[0], s, r, t);
+    for (int base = 0; base < npad; base += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int it = base + j;
+        const int sl = (it + 1) % NSLOT;
+        put_x((j + 1) % PF, sl);
+        __syncthreads();
+        load_stage((j + PF - 1) % PF);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
+        if (it < n_it) {
+          const uint8_t* tab[T];
+          tables(tab);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
+          after_chunk(it);
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+          for (int g = 0; g < G; ++g) bc[s][g] = bn[s][g];
+      }
+    }
+  } else {
+    for (int base = 0; base < npad; base += PF) {
+#pragma unroll
+      for (int j = 0; j < PF; ++j) {
+        const int it = base + j;
+        put_x(j, it & 1);
+        __syncthreads();
+        load_stage((j + PF - 1) % PF);
+        if (it < n_it) {
+          const uint8_t* tab[T];
+          tables(tab);
+          compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
+          after_chunk(it);
         }
       }
     }
-    f32x4 acc[T][G];
-#pragma unroll
-    for (int i = 0; i < T; ++i)
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc[i][g] = acc2[0][i][g] + acc2[1][i][g];
-
-    if (c0 == 0 && c1 == a.C) {
-      epilogue<G, PAIR, OUTF32>(a, mi, wtile0, acc, r, t);
-      __syncthreads();
-      continue;
-    }
-
-    // Split tile group: publish this workgroup's partial (float e of thread tid at [e][tid]), count arrivals;
-    // the last workgroup adds all partials in workgroup order and applies the epilogue. The exchange uses
-    // agent-coherent accesses instead of fences: the partials are stored and loaded with agent-scope relaxed
-    // atomics (write-through past the XCD's L2, and reads that do not hit a stale L2 line), each thread waits
-    // for its stores to complete before the barrier, and only then does thread 0 count the arrival. No
-    // L2-wide writeback or invalidate is needed.
-    const int pf = wg_of_unit(static_cast<long long>(tg) * a.C, a.P, a.U);
-    const int pl = wg_of_unit(static_cast<long long>(tg) * a.C + a.C - 1, a.P, a.U);
-    constexpr int SLOT = NACC * kThreads;
-    float* slotp = a.partials + static_cast<size_t>(2 * p + (tg == tg_first ? 0 : 1)) * SLOT + threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < T; ++i)
-#pragma unroll
-      for (int g = 0; g < G; ++g)
-        if (16 * g + r < a.M)
-#pragma unroll
-          for (int v = 0; v < 4; ++v)
-            __hip_atomic_store(slotp + ((i * G + g) * 4 + v) * kThreads, acc[i][g][v], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const int old = __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last_flag = old == pl - pf;
-      if (last_flag) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (last_flag) {
-      // partials in workgroup order; QB of them in flight at a time (loads may complete in any order, the adds
-      // are in order)
-      constexpr int QB = NACC <= 8 ? 8 : NACC <= 16 ? 4 : 2;
-      for (int q0 = pf; q0 <= pl; q0 += QB) {
-        float pv[QB][NACC];
-#pragma unroll
-        for (int b = 0; b < QB; ++b) {
-          const int q = q0 + b;
-          if (q <= pl) {
-            const int qf = static_cast<int>(unit_start(q, a.P, a.U) / a.C);
-            const float* sq = a.partials + static_cast<size_t>(2 * q + (tg == qf ? 0 : 1)) * SLOT + threadIdx.x;
-#pragma unroll
-            for (int e = 0; e < NACC; ++e)
-              pv[b][e] = (16 * ((e >> 2) % G) + r < a.M)
-                             ? __hip_atomic_load(sq + e * kThreads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                             : 0.f;
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < QB; ++b) {
-          const int q = q0 + b;
-          if (q <= pl) {
-#pragma unroll
-            for (int i = 0; i < T; ++i)
-#pragma unroll
-              for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                  const float x = pv[b][(i * G + g) * 4 + v];
-                  acc[i][g][v] = (q == pf) ? x : acc[i][g][v] + x;
-                }
-          }
-        }
-      }
-      epilogue<G, PAIR, OUTF32>(a, mi, wtile0, acc, r, t);
-    }
-    __syncthreads();
   }
+  f32x4 accL[T][G];
+  fold(accL);
+
+  // Finish the first and the last tile group of the range: a whole one directly, a split one through the
+  // partial exchange (every workgroup publishes, counts its arrival, and the last to arrive adds them).
+  const bool one = tg_first == tg_last;
+  const bool splitF = !one && cfirst != 0;
+  const int lbeg = one ? cfirst : 0;
+  const int lend = u1 - tg_last * a.C;
+  const bool splitL = !(lbeg == 0 && lend == a.C);
+  if (!one) {
+    if (splitF) publish_partial<G, T>(a, p, 0, accF, r);
+    else epilogue<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+  }
+  if (splitL) publish_partial<G, T>(a, p, one ? 0 : 1, accL, r);
+  else epilogue<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, accL, eL, r, t);
+  if (!splitF && !splitL) return;
+  // Each thread waits for its own partial stores to complete before the barrier; only then does thread 0
+  // count the workgroup's arrival.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const SplitInfo si[2] = {split_info(a, tg_first), split_info(a, tg_last)};
+  if (threadIdx.x < 2) {
+    const int h = threadIdx.x;
+    const int tg = h == 0 ? tg_first : tg_last;
+    int last = 0;
+    if (h == 0 ? splitF : splitL) {
+      const int old = __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == si[h].pl - si[h].pf;
+      if (last) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    last_flag[h] = last;
+  }
+  __syncthreads();
+  const bool doit[2] = {last_flag[0] != 0, last_flag[1] != 0};
+  if (!doit[0] && !doit[1]) return;
+  reduce_partials<G, T>(a, p, doit, si, accF, accL, r);
+  if (doit[0]) epilogue<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+  if (doit[1]) epilogue<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, accL, eL, r, t);
 }
 
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
@@ -559,6 +734,10 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     if (m.N <= 0 || m.N % 16 != 0) return fail(LQ_ERR_SHAPE, nm + ": N % 16 and K % 128 must be 0");
     if (!m.w || !m.y) return fail(LQ_ERR_ARG, nm + ": null weight or output");
     if (fmt == kFp4Coded && !m.table) return fail(LQ_ERR_ARG, nm + ": null scale-code table");
+    // the epilogue reads 4 channels' scales as one 16-byte load and writes 4 outputs as one 8- or 16-byte store
+    if (reinterpret_cast<uintptr_t>(m.svec) % 16 != 0 || reinterpret_cast<uintptr_t>(m.y) % (outf32 ? 16 : 8) != 0 ||
+        reinterpret_cast<uintptr_t>(m.resid) % 8 != 0 || m.ldy % 4 != 0)
+      return fail(LQ_ERR_ARG, nm + ": scales must be 16-byte aligned, outputs and residual 8-byte aligned");
     a.w[i] = m.w;
     a.table[i] = m.table;
     a.svec[i] = m.svec;
@@ -576,8 +755,10 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   }
   a.tg0[n] = tg;
   a.TG = tg;
-  a.U = static_cast<long long>(tg) * a.C;
-  a.P = choose_wgs(a.U);
+  const long long units = static_cast<long long>(tg) * a.C;
+  a.P = choose_wgs(units);
+  if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrices too large for one launch");
+  a.U = static_cast<int>(units);
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
   const size_t slot_floats = static_cast<size_t>(2) * cdiv(M, 16) * 4 * kThreads;
