@@ -623,16 +623,18 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   const SplitInfo si[2] = {split_info(a, tg_first), split_info(a, tg_last)};
+  // (selects rather than indexing si by thread: a thread-indexed local array would be placed in LDS)
   if (threadIdx.x < 2) {
-    const int h = threadIdx.x;
-    const int tg = h == 0 ? tg_first : tg_last;
+    const bool h = threadIdx.x != 0;
+    const int tg = h ? tg_last : tg_first;
+    const int span = h ? si[1].pl - si[1].pf : si[0].pl - si[0].pf;
     int last = 0;
-    if (h == 0 ? splitF : splitL) {
+    if (h ? splitL : splitF) {
       const int old = __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = old == si[h].pl - si[h].pf;
+      last = old == span;
       if (last) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    last_flag[h] = last;
+    last_flag[h ? 1 : 0] = last;
   }
   __syncthreads();
   const bool doit[2] = {last_flag[0] != 0, last_flag[1] != 0};
