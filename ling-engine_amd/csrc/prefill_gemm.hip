@@ -7,18 +7,20 @@
 // src/core/stream_gemm.cu:705-738), with one FP32 scale per 128x128 block, ws [N/128][K/128].
 //
 // Design:
-//  * One v_mfma_f32_16x16x128_f8f6f4 per 16x16 output tile per 128-value K block: an MFMA covers exactly one
+//  * One v_mfma_scale_f32_16x16x128_f8f6f4 per 16x16 output tile per 128-value K block: an MFMA covers exactly one
 //    scale block, so its FP32 result is scaled once and added to the accumulator (one FMA per output per
 //    block). Any permutation of K inside the block is harmless, since A and B use the same one.
-//  * Weights are the A operand (rows n) and activations the B operand (columns m): a lane's four outputs
-//    share one token and one 128-row weight block, so its block scale is one multiply per token tile.
-//  * A workgroup (8 waves, 2 per SIMD: 2 along the weights x 4 along the tokens) computes 128 weight rows x
-//    256 tokens; each wave 64 x 64 (4 x 4 MFMA tiles). Each K block's operands (16 KB of weights, 32 KB of
-//    activations) are staged in LDS (double buffered) as [row][8 x 16-byte units] with the unit index
-//    XOR-swizzled by row, so the fragment reads are bank-conflict free. Global loads run two K blocks ahead
-//    through two register staging sets: a block's loads are issued two iterations before it is written to
-//    LDS and computed.
-//  * Tile order: each XCD works through a contiguous range of a grouped raster (8 weight tiles x every
+//  * Weights are the A operand (rows n) and activations the B operand (columns m). A workgroup (8 waves, 2 per
+//    SIMD: 2 along the weights x 4 along the tokens) computes 256 weight rows x 256 tokens; each wave 128 x 64
+//    (8 x 4 MFMA tiles, 128 accumulator registers). A wave's 128 weight rows are one weight scale block, so
+//    the block scale is a scalar and each lane's scale is that scalar times its token's activation scale.
+//  * Operands reach LDS without passing through registers: buffer loads with the LDS flag write each lane's
+//    16 bytes at the next 16 bytes of a 1 KB run, and the lane-to-source map implements the layout: a K
+//    block of a 256-row operand is [row][8 x 16-byte units] with the unit index XOR-swizzled by the row, so
+//    the fragment reads are bank-conflict free. The block's activation scales come along the same way.
+//  * Two LDS stages (65 KB each): while a K block is computed from one, the next block's loads fill the
+//    other. The waits are explicit: the compiler cannot see which LDS bytes a load-to-LDS writes.
+//  * Tile order: each XCD works through a contiguous range of a grouped raster (kGroupN weight tiles x every
 //    token tile per group), so the workgroups running at once on an XCD share the K slices of both operands
 //    in its L2 instead of re-streaming the whole activation matrix per weight tile.
 #include "lq_common.hpp"
@@ -29,14 +31,17 @@
 namespace lq {
 namespace {
 
-constexpr int kBN = 128;  // weight rows per workgroup
+constexpr int kBN = 256;  // weight rows per workgroup
 constexpr int kBM = 256;  // tokens per workgroup
 constexpr int kThreads = 512;
-constexpr int kGroupN = 8;  // weight tiles per raster group
-constexpr int kRowBytes = 128;                       // one K block of one row (FP8)
-constexpr int kStage = (kBN + kBM) * kRowBytes;      // 48 KB: weights then activations
+constexpr int kGroupN = 4;                       // weight tiles per raster group
+constexpr int kRowBytes = 128;                   // one K block of one row (FP8)
+constexpr int kOpBytes = 256 * kRowBytes;        // one operand's K block in LDS: 32 KB
+constexpr int kStage = 2 * kOpBytes + kBM * 4;   // weights, activations, activation scales: 65 KB
 
 // Byte offset of 16-byte unit u of row `row` in an LDS operand tile.
+// A fragment read serves 16 lanes (rows r .. r + 15, one unit each) per 256-byte LDS cycle: bank group
+// (row % 2) * 8 + swizzled unit is then distinct across the 16 rows.
 __device__ __forceinline__ int lds_off(int row, int u) { return row * kRowBytes + ((u ^ ((row >> 1) & 7)) << 4); }
 
 struct PrefillArgs {
@@ -49,16 +54,27 @@ struct PrefillArgs {
   int tiles_m, tiles_n;
 };
 
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 4, voff, soff, 0, 0);
+}
+// s_waitcnt with only vmcnt / lgkmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
+#define LQ_WAIT_VM0() __builtin_amdgcn_s_waitcnt(0x0f70)
+#define LQ_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xc07f)
+
 __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, t = lane >> 4;
-  const int wn = wave & 1, wm = wave >> 1;  // wave's 64-row weight half and 64-token quarter
+  const int wn = wave & 1, wm = wave >> 1;  // the wave's 128-row weight half and 64-token quarter
 
   // Tile order. The hardware places block b on XCD b % 8; each XCD takes a contiguous range of the logical
   // tile order, in which tiles come in groups of kGroupN weight tiles x all token tiles, token tile slowest
-  // within a group. The ~32 workgroups an XCD runs at once then cover kGroupN weight tiles x a few token
-  // tiles, so the K slices of both operands they read at a time are shared in that XCD's L2.
+  // within a group.
   const int nb = gridDim.x, b = blockIdx.x;
   int tile = b;
   if ((nb & 7) == 0) tile = (b & 7) * (nb >> 3) + (b >> 3);
@@ -69,125 +85,117 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
 
   const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0x7fffffff, 0x00020000);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.xq), 0, 0x7fffffff, 0x00020000);
-
-  // Global -> LDS copy plan, 2 + 4 16-byte pieces per thread and K block.
-  // Weights: piece j (0..1023) = tiled block (16-row tile tw = j / 128, piece p = j % 128) of the current chunk;
-  // p = ((h*2 + q)*8 + g)*4 + tt holds row g + 8h, values [32 tt + 16 q, +16): LDS row 16 tw + g + 8h, unit 2 tt + q.
-  constexpr int WP = kBN * kRowBytes / 16 / kThreads, XP = kBM * kRowBytes / 16 / kThreads;
-  int wsrc[WP], wdst[WP], xsrc[XP], xdst[XP];
-#pragma unroll
-  for (int i = 0; i < WP; ++i) {
-    const int j = i * kThreads + threadIdx.x;
-    const int tw = j >> 7, p = j & 127;
-    const int tt = p & 3, g = (p >> 2) & 7, q = (p >> 5) & 1, h = p >> 6;
-    wsrc[i] = ((n0 >> 4) + tw) * a.KB * kTileBytesFp8 + p * 16;
-    wdst[i] = lds_off(16 * tw + g + 8 * h, 2 * tt + q);
-  }
-#pragma unroll
-  for (int i = 0; i < XP; ++i) {
-    // activations: row j / 8 of the token tile, unit j % 8 (rows past M read as zeros, out of range)
-    const int j = i * kThreads + threadIdx.x;
-    const int row = j >> 3, u = j & 7, m = m0 + row;
-    xsrc[i] = m < a.M ? m * a.K + u * 16 : static_cast<int>(0x80000000u);
-    xdst[i] = kBN * kRowBytes + lds_off(row, u);
-  }
-
-  // per-lane block-scale inputs: this lane's four tokens (one per token tile); their activation scales travel
-  // with the block's operands (loaded into the same staging set), so waiting for a scale never waits for a
-  // later block's prefetch (loads retire in issue order)
-  int xso[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xso[j] = min(m0 + wm * 64 + 16 * j + r, a.M - 1) * a.KB * 4;
   const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xs), 0, 0x7fffffff, 0x00020000);
-  const float* wsrow = a.ws + static_cast<size_t>(tn) * a.KB;
 
-  u32x4 stg[2][WP + XP];
-  float xsc[2][4];
-  auto load = [&](int sset, int kb) {
-    const unsigned oob = kb < a.KB ? 0u : 0x80000000u;
+  // Load-to-LDS plan: load i (0..3) of wave w writes LDS bytes [((i * 8 + w) * 64 + lane) * 16, +16) of an
+  // operand tile: row = (i * 8 + w) * 8 + lane / 8, swizzled unit lane % 8, i.e. source unit u = lane % 8 ^ (row / 2 % 8).
+  // Weights: row's 16-row tile tw and row rr in it; unit u = 2 tt + q sits at tiled piece ((h*2 + q)*8 + g)*4 + tt
+  // (g = rr % 8, h = rr / 8). Rows past N or M read out of range (nothing is loaded for them).
+  int wsrc[4], xsrc[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      xsc[sset][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, static_cast<int>(xso[j] | oob), kb * 4, 0));
+  for (int i = 0; i < 4; ++i) {
+    const int row = (i * 8 + wave) * 8 + (lane >> 3), u = (lane & 7) ^ ((row >> 1) & 7);
+    const int tw = row >> 4, rr = row & 15, g = rr & 7, h = rr >> 3, tt = u >> 1, q = u & 1;
+    const int p = ((h * 2 + q) * 8 + g) * 4 + tt;
+    wsrc[i] = n0 + row < a.N ? ((n0 >> 4) + tw) * a.KB * kTileBytesFp8 + p * 16 : static_cast<int>(0x80000000u);
+    const int m = m0 + row;
+    xsrc[i] = m < a.M ? m * a.K + u * 16 : static_cast<int>(0x80000000u);
+  }
+  // activation scales: waves 0-3 load one token's scale per lane
+  const int srow = wave * 64 + lane;
+  const int ssrc = (wave < 4 && m0 + srow < a.M) ? (m0 + srow) * a.KB * 4 : static_cast<int>(0x80000000u);
+
+  auto issue = [&](int st, int kb) {
+    uint8_t* base = smem + st * kStage;
 #pragma unroll
-    for (int i = 0; i < WP; ++i)
-      stg[sset][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, static_cast<int>(wsrc[i] | oob), kb * kTileBytesFp8, 0));
+    for (int i = 0; i < 4; ++i) dma16(wr, base + (i * 8 + wave) * 1024, wsrc[i], kb * kTileBytesFp8);
 #pragma unroll
-    for (int i = 0; i < XP; ++i)
-      stg[sset][WP + i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, static_cast<int>(xsrc[i] | oob), kb * kRowBytes, 0));
-  };
-  auto store = [&](int sset, uint8_t* st) {
-#pragma unroll
-    for (int i = 0; i < WP; ++i) *reinterpret_cast<u32x4*>(st + wdst[i]) = stg[sset][i];
-#pragma unroll
-    for (int i = 0; i < XP; ++i) *reinterpret_cast<u32x4*>(st + xdst[i]) = stg[sset][WP + i];
+    for (int i = 0; i < 4; ++i) dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc[i], kb * kRowBytes);
+    if (wave < 4) dma4(sr, base + 2 * kOpBytes + wave * 256, ssrc, kb * 4);
   };
 
-  f32x4 acc[4][4];
+  f32x4 acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // K block kb: loaded into staging set kb % 2 two iterations ahead, written to LDS buffer kb % 2, computed.
-  // LDS buffer kb % 2 was last read by block kb - 2, which every wave finished before the barrier of kb - 1.
-  load(0, 0);
-  load(1, 1);
-  const int KBP = (a.KB + 1) & ~1;
-  for (int kb0 = 0; kb0 < KBP; kb0 += 2) {
+  const float* wsrow = a.ws + static_cast<size_t>((n0 >> 7) + wn) * a.KB;
+  const bool wrows = n0 + wn * 128 < a.N;  // this wave's weight half exists
+
+  // Fragment reads from an LDS stage: weight tile i (rows wn*128 + 16i + r) and token tile j (rows wm*64 + 16j
+  // + r), 32 bytes at K 32t each.
+  auto frag = [&](const uint8_t* op, int row) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(op + lds_off(row, 2 * t));
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(op + lds_off(row, 2 * t + 1));
+    return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+  i32x8 bf[4], af;
+  float sc[4];
+  f32x4 pr[4];
+  // B fragments, the lane's four block scales and the first A fragment of K block kb (stage st)
+  auto block_start = [&](int st, int kb) {
+    const uint8_t* sa = smem + st * kStage;
+    const float* sxs = reinterpret_cast<const float*>(sa + 2 * kOpBytes);
+    const float wsc = wrows ? wsrow[kb] : 0.f;
+    af = frag(sa, wn * 128 + r);
 #pragma unroll
-    for (int ph = 0; ph < 2; ++ph) {
-      const int kb = kb0 + ph;
-      uint8_t* st = smem + ph * kStage;
-      store(ph, st);
-      // the block's combined scales, taken before this staging set is refilled
-      const float wsc = kb < a.KB ? wsrow[kb] : 0.f;
-      float sc[4];
+    for (int j = 0; j < 4; ++j) bf[j] = frag(sa + kOpBytes, wm * 64 + 16 * j + r);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = xsc[ph][j] * wsc;
-      __syncthreads();
-      load(ph, kb + 2);  // out-of-range blocks load nothing
-      if (kb < a.KB) {
-        // fragments: weights rows wn*64 + 16i + r, activations rows wm*64 + 16j + r; 32 bytes at K 32t
-        i32x8 af[4], bf[4];
+    for (int j = 0; j < 4; ++j) sc[j] = sxs[wm * 64 + 16 * j + r] * wsc;
+  };
+  auto fold = [&](f32x4 (&dst)[4], const f32x4 (&p)[4], const float (&s)[4]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int row = wn * 64 + 16 * i + r;
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t));
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(st + lds_off(row, 2 * t + 1));
-          af[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int row = wm * 64 + 16 * j + r;
-          const uint8_t* xb = st + kBN * kRowBytes;
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t));
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(xb + lds_off(row, 2 * t + 1));
-          bf[j] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
+      for (int v = 0; v < 4; ++v) dst[j][v] = __builtin_fmaf(p[j][v], s[j], dst[j][v]);
+  };
+
+  issue(0, 0);
+  LQ_WAIT_VM0();
+  __builtin_amdgcn_s_barrier();
+  block_start(0, 0);
+  // Per K block and weight tile: the tile's four MFMAs, then the next tile's fragment read, then the fold of
+  // the four results into the accumulators (the other wave on the SIMD issues its MFMAs meanwhile). The one
+  // barrier per block sits after tile 7's MFMAs are issued: it publishes the next block's loads and frees this
+  // block's stage for its refill. Empty volatile statements pin this order (the compiler would otherwise sink
+  // the MFMAs to their use, hoist the reads and defer the folds, and run out of registers).
+  for (int kb = 0; kb < a.KB; ++kb) {
+    const int st = kb & 1;
+    const uint8_t* sa = smem + st * kStage;
+    if (kb + 1 < a.KB) issue(st ^ 1, kb + 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
-            const f32x4 p = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf[j], f32x4{0.f, 0.f, 0.f, 0.f},
-                                                                            0, 0, 0, 127, 0, 127);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) acc[i][j][v] = __builtin_fmaf(p[v], sc[j], acc[i][j][v]);
-          }
+      for (int j = 0; j < 4; ++j)
+        // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
+        pr[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
+                                                                0, 127);
+      asm volatile("" ::"v"(pr[0]), "v"(pr[1]), "v"(pr[2]), "v"(pr[3]) : "memory");
+      if (i < 7) {
+        af = frag(sa, wn * 128 + 16 * (i + 1) + r);
+      } else {
+        // every wave's reads of this stage have returned and its loads of the next block have landed
+        LQ_WAIT_LGKM0();
+        LQ_WAIT_VM0();
+        __builtin_amdgcn_s_barrier();
       }
+      asm volatile("" ::: "memory");
+      fold(acc[i], pr, sc);
+      asm volatile("" ::"v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]));
     }
+    if (kb + 1 < a.KB) block_start(st ^ 1, kb + 1);
   }
 
-  // epilogue: lane holds rows n = n0 + wn*64 + 16i + 4t + v, token m = m0 + wm*64 + 16j + r
+  // epilogue: lane holds rows n = n0 + wn*128 + 16i + 4t + v, token m = m0 + wm*64 + 16j + r
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int m = m0 + wm * 64 + 16 * j + r;
     if (m >= a.M) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = n0 + wn * 64 + 16 * i + 4 * t;
+    for (int i = 0; i < 8; ++i) {
+      const int n = n0 + wn * 128 + 16 * i + 4 * t;
+      if (n >= a.N) continue;
       uint16_t* dst = a.y + static_cast<size_t>(m) * a.ldy + n;
       *reinterpret_cast<u32x2*>(dst) = u32x2{f32_to_bf16(acc[i][j][0]) | (uint32_t(f32_to_bf16(acc[i][j][1])) << 16),
                                              f32_to_bf16(acc[i][j][2]) | (uint32_t(f32_to_bf16(acc[i][j][3])) << 16)};
@@ -253,9 +261,9 @@ int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_
   a.K = K;
   a.KB = K / 128;
   a.tiles_m = cdiv(M, kBM);
-  a.tiles_n = N / kBN;
+  a.tiles_n = cdiv(N, kBN);
   const long long blocks = static_cast<long long>(a.tiles_m) * a.tiles_n;
-  // 96 KB of dynamic LDS is above the default per-launch limit; raise it (idempotent, per process).
+  // 130 KB of dynamic LDS is above the default per-launch limit; raise it (idempotent, per process).
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_fp8_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                           2 * kStage);
