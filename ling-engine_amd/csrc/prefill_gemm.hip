@@ -105,13 +105,24 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   const int srow = wave * 64 + lane;
   const int ssrc = (wave < 4 && m0 + srow < a.M) ? (m0 + srow) * a.KB * 4 : static_cast<int>(0x80000000u);
 
-  auto issue = [&](int st, int kb) {
+  // A block's loads come in 5 parts (weights 0-1, 2-3, activations 0-1, 2-3, scales), issued one per tile
+  // rather than in one burst, which would stall the waves on a full memory queue.
+  auto issue_part = [&](int st, int kb, int part) {
     uint8_t* base = smem + st * kStage;
+    if (part < 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(wr, base + (i * 8 + wave) * 1024, wsrc[i], kb * kTileBytesFp8);
+      for (int i = 2 * part; i < 2 * part + 2; ++i) dma16(wr, base + (i * 8 + wave) * 1024, wsrc[i], kb * kTileBytesFp8);
+    } else if (part < 4) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc[i], kb * kRowBytes);
-    if (wave < 4) dma4(sr, base + 2 * kOpBytes + wave * 256, ssrc, kb * 4);
+      for (int i = 2 * (part - 2); i < 2 * (part - 2) + 2; ++i)
+        dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc[i], kb * kRowBytes);
+    } else if (wave < 4) {
+      dma4(sr, base + 2 * kOpBytes + wave * 256, ssrc, kb * 4);
+    }
+  };
+  auto issue = [&](int st, int kb) {
+#pragma unroll
+    for (int part = 0; part < 5; ++part) issue_part(st, kb, part);
   };
 
   f32x4 acc[8][4];
@@ -163,9 +174,9 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   for (int kb = 0; kb < a.KB; ++kb) {
     const int st = kb & 1;
     const uint8_t* sa = smem + st * kStage;
-    if (kb + 1 < a.KB) issue(st ^ 1, kb + 1);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
+      if (i < 5 && kb + 1 < a.KB) issue_part(st ^ 1, kb + 1, i);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
