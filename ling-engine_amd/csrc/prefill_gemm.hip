@@ -83,24 +83,22 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   const int tn = grp * kGroupN + rem % gsize, tm = rem / gsize;
   const int n0 = tn * kBN, m0 = tm * kBM;
 
-  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.xq), 0, 0x7fffffff, 0x00020000);
-  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xs), 0, 0x7fffffff, 0x00020000);
+  // Buffer resources sized to the operands: loads past the end (rows past N or M) return nothing.
+  const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w), 0, a.N * a.K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.xq), 0, a.M * a.K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xs), 0, a.M * a.KB * 4, 0x00020000);
 
   // Load-to-LDS plan: load i (0..3) of wave w writes LDS bytes [((i * 8 + w) * 64 + lane) * 16, +16) of an
-  // operand tile: row = (i * 8 + w) * 8 + lane / 8, swizzled unit lane % 8, i.e. source unit u = lane % 8 ^ (row / 2 % 8).
-  // Weights: row's 16-row tile tw and row rr in it; unit u = 2 tt + q sits at tiled piece ((h*2 + q)*8 + g)*4 + tt
-  // (g = rr % 8, h = rr / 8). Rows past N or M read out of range (nothing is loaded for them).
-  int wsrc[4], xsrc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (i * 8 + wave) * 8 + (lane >> 3), u = (lane & 7) ^ ((row >> 1) & 7);
-    const int tw = row >> 4, rr = row & 15, g = rr & 7, h = rr >> 3, tt = u >> 1, q = u & 1;
-    const int p = ((h * 2 + q) * 8 + g) * 4 + tt;
-    wsrc[i] = n0 + row < a.N ? ((n0 >> 4) + tw) * a.KB * kTileBytesFp8 + p * 16 : static_cast<int>(0x80000000u);
-    const int m = m0 + row;
-    xsrc[i] = m < a.M ? m * a.K + u * 16 : static_cast<int>(0x80000000u);
-  }
+  // operand tile: row = (i * 8 + w) * 8 + lane / 8, swizzled unit lane % 8, i.e. source unit u = lane % 8 ^ (row / 2 % 8)
+  // (the same for every i, as i moves the row by 64). Weights: the row's 16-row tile tw and row rr in it; unit
+  // u = 2 tt + q sits at tiled piece ((h*2 + q)*8 + g)*4 + tt (g = rr % 8, h = rr / 8); load i is 4 tiles on.
+  // Activations: row-major, load i is 64 rows on. The per-i and per-block steps go in the scalar offset.
+  const int row0 = wave * 8 + (lane >> 3), u0 = (lane & 7) ^ ((row0 >> 1) & 7);
+  const int wsrc = (((n0 >> 4) + (row0 >> 4)) * a.KB) * kTileBytesFp8 +
+                   (((((row0 & 15) >> 3) * 2 + (u0 & 1)) * 8 + (row0 & 7)) * 4 + (u0 >> 1)) * 16;
+  const int xsrc = (m0 + row0) * a.K + u0 * 16;
+  const int wstep = 4 * a.KB * kTileBytesFp8, xstep = 64 * a.K;
   // activation scales: waves 0-3 load one token's scale per lane
   const int srow = wave * 64 + lane;
   const int ssrc = (wave < 4 && m0 + srow < a.M) ? (m0 + srow) * a.KB * 4 : static_cast<int>(0x80000000u);
@@ -111,11 +109,12 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
     uint8_t* base = smem + st * kStage;
     if (part < 2) {
 #pragma unroll
-      for (int i = 2 * part; i < 2 * part + 2; ++i) dma16(wr, base + (i * 8 + wave) * 1024, wsrc[i], kb * kTileBytesFp8);
+      for (int i = 2 * part; i < 2 * part + 2; ++i)
+        dma16(wr, base + (i * 8 + wave) * 1024, wsrc, kb * kTileBytesFp8 + i * wstep);
     } else if (part < 4) {
 #pragma unroll
       for (int i = 2 * (part - 2); i < 2 * (part - 2) + 2; ++i)
-        dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc[i], kb * kRowBytes);
+        dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc, kb * kRowBytes + i * xstep);
     } else if (wave < 4) {
       dma4(sr, base + 2 * kOpBytes + wave * 256, ssrc, kb * 4);
     }
@@ -259,6 +258,9 @@ int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_
     return fail(LQ_ERR_SHAPE, "prefill_gemm: N % 128 and K % 128 must be 0");
   if (M < 1) return LQ_OK;  // nothing to do (the reference returns silently)
   if (ldy < N || ldy % 4 != 0) return fail(LQ_ERR_SHAPE, "prefill_gemm: ldy must be >= N and a multiple of 4");
+  // operand byte offsets are 32-bit
+  if (static_cast<long long>(N) * K >= (1LL << 31) || static_cast<long long>(M) * K >= (1LL << 31))
+    return fail(LQ_ERR_SHAPE, "prefill_gemm: N * K and M * K must be below 2^31");
   if (!xq || !xs || !w || !ws || !y) return fail(LQ_ERR_ARG, "prefill_gemm: null pointer");
   PrefillArgs a{};
   a.xq = xq;
