@@ -80,6 +80,11 @@ int lq_dequant_tiled_nvfp4_f32(const uint8_t* tw, float scale2, float* out, int 
 int lq_to_half_rows(const float* x, int M, int K, uint16_t* xh, float* xinv, void* stream);
 /* The same from BF16 x. kernels.cuh:546-547 bf16_to_half_rows */
 int lq_bf16_to_half_rows(const uint16_t* x, int M, int K, uint16_t* xh, float* xinv, void* stream);
+/* RMSNorm of each row: out = x * rstd * w' (FP32 [rows][H]; rstd = 1 / sqrt(mean(x^2) + eps), w' = 1 + w when
+ * gemma, else w; w BF16 [H]) and the FP16 row copy of out with its row scales, as to_half_rows makes them.
+ * kernels.cuh:267-268 rmsnorm_half */
+int lq_rmsnorm_half(const float* x, const uint16_t* w, float* out, uint16_t* xh, float* xinv, int rows, int H, float eps,
+                    int gemma, void* stream);
 /* y[M][N] (FP32) = (wscale * xh . W^T) * xinv[m], W tiled FP8. kernels.cuh:276-277 stream_gemm_fp8 */
 int lq_stream_gemm_fp8(const uint16_t* xh, const float* xinv, int M, const uint8_t* w, float wscale, float* y, int N,
                        int K, void* stream);
@@ -127,6 +132,18 @@ int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* sc
  * (kernels.cuh:213-214) and prefill_gemm_fp8_bf16out (kernels.cuh:239-240). */
 int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws, uint16_t* y,
                          int ldy, int N, int K, void* stream);
+
+/* ---------------- prefill, per-tensor FP8 (reference src/core/kernels.cuh:190-221,239-240) ---------------- */
+/* FP32 x [M][K] -> FP8 E4M3 q = E4M3_satfinite(bf16(x) * (1 / input_scale)). K % 4 == 0.
+ * kernels.cuh:199 quant_act_fp8 */
+int lq_quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q, void* stream);
+/* y[M][0..N) (FP32, rows ldy apart) = alpha * xq . W^T, or += with accumulate; W tiled FP8. N % 128 == 0,
+ * K % 128 == 0; M < 1 does nothing. kernels.cuh:213-214 prefill_gemm_fp8 */
+int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
+                        int accumulate, void* stream);
+/* The same rounded to BF16 (never accumulated). kernels.cuh:239-240 prefill_gemm_fp8_bf16out */
+int lq_prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, float alpha, uint16_t* y, int ldy, int N,
+                                int K, void* stream);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,10 @@ inline void to_half_rows(const float* x, int M, int K, __half* out, float* xinv,
 inline void bf16_to_half_rows(const uint16_t* x_bf16, int M, int K, __half* out, float* xinv, hipStream_t s) {
   lq_check(lq_bf16_to_half_rows(x_bf16, M, K, reinterpret_cast<uint16_t*>(out), xinv, s));
 }
+inline void rmsnorm_half(const float* x, const uint16_t* w_bf16, float* out, __half* xh, float* xinv, int rows, int H,
+                         float eps, bool gemma, hipStream_t s) {
+  lq_check(lq_rmsnorm_half(x, w_bf16, out, reinterpret_cast<uint16_t*>(xh), xinv, rows, H, eps, gemma ? 1 : 0, s));
+}
 inline void stream_gemm_nvfp4(const __half* x, const float* xinv, int M, const uint8_t* w, const uint8_t* wscale,
                               float scale2, float* y, int N, int K, hipStream_t s) {
   lq_check(lq_stream_gemm_nvfp4(reinterpret_cast<const uint16_t*>(x), xinv, M, w, wscale, scale2, y, N, K, s));
@@ -100,6 +104,17 @@ inline void stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const 
 // ---- prefill (block-scaled FP8; kernels.cuh:190-221 for the reference's per-tensor forms) ----
 inline void quant_act_fp8_g128(const uint16_t* x_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t s) {
   lq_check(lq_quant_act_fp8_g128(x_bf16, M, K, q, scale, s));
+}
+inline void quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q, hipStream_t s) {
+  lq_check(lq_quant_act_fp8(x, M, K, input_scale, q, s));
+}
+inline void prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
+                             bool accumulate, hipStream_t s) {
+  lq_check(lq_prefill_gemm_fp8(xq, M, w, alpha, y, ldy, N, K, accumulate ? 1 : 0, s));
+}
+inline void prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, float alpha, uint16_t* y_bf16, int ldy,
+                                     int N, int K, hipStream_t s) {
+  lq_check(lq_prefill_gemm_fp8_bf16out(xq, M, w, alpha, y_bf16, ldy, N, K, s));
 }
 inline void prefill_gemm_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws,
                                    uint16_t* y_bf16, int ldy, int N, int K, hipStream_t s) {

@@ -46,13 +46,17 @@ __device__ __forceinline__ int lds_off(int row, int u) { return row * kRowBytes 
 
 struct PrefillArgs {
   const uint8_t* xq;
-  const float* xs;
+  const float* xs;  // block-scaled: activation group scales [M][K/128]
   const uint8_t* w;
-  const float* ws;
-  uint16_t* y;
+  const float* ws;  // block-scaled: weight block scales [N/128][K/128]
+  float alpha;      // per-tensor: the one scale (input scale x weight scale)
+  void* y;          // BF16 or FP32 [M][ldy]
   int ldy, M, N, K, KB;
   int tiles_m, tiles_n;
 };
+
+// Output of a prefill GEMM: BF16, FP32, or FP32 added to what y holds.
+enum PrefillOut { kOutBf16 = 0, kOutF32 = 1, kOutF32Acc = 2 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -66,6 +70,10 @@ __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, in
 #define LQ_WAIT_VM0() __builtin_amdgcn_s_waitcnt(0x0f70)
 #define LQ_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xc07f)
 
+// BLOCK: the block-scaled form (each 128-value block's product scaled by its activation and weight scales and
+// folded into the accumulators); else one scale for the whole product, applied at the end, and the MFMAs
+// accumulate across K themselves.
+template <bool BLOCK, int OUT>
 __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -115,7 +123,7 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
 #pragma unroll
       for (int i = 2 * (part - 2); i < 2 * (part - 2) + 2; ++i)
         dma16(xr, base + kOpBytes + (i * 8 + wave) * 1024, xsrc, kb * kRowBytes + i * xstep);
-    } else if (wave < 4) {
+    } else if (BLOCK && wave < 4) {
       dma4(sr, base + 2 * kOpBytes + wave * 256, ssrc, kb * 4);
     }
   };
@@ -130,7 +138,7 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const float* wsrow = a.ws + static_cast<size_t>((n0 >> 7) + wn) * a.KB;
+  const float* wsrow = BLOCK ? a.ws + static_cast<size_t>((n0 >> 7) + wn) * a.KB : nullptr;
   const bool wrows = n0 + wn * 128 < a.N;  // this wave's weight half exists
 
   // Fragment reads from an LDS stage: weight tile i (rows wn*128 + 16i + r) and token tile j (rows wm*64 + 16j
@@ -147,12 +155,14 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   auto block_start = [&](int st, int kb) {
     const uint8_t* sa = smem + st * kStage;
     const float* sxs = reinterpret_cast<const float*>(sa + 2 * kOpBytes);
-    const float wsc = wrows ? wsrow[kb] : 0.f;
+    const float wsc = (BLOCK && wrows) ? wsrow[kb] : 0.f;
     af = frag(sa, wn * 128 + r);
 #pragma unroll
     for (int j = 0; j < 4; ++j) bf[j] = frag(sa + kOpBytes, wm * 64 + 16 * j + r);
+    if constexpr (BLOCK) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sc[j] = sxs[wm * 64 + 16 * j + r] * wsc;
+      for (int j = 0; j < 4; ++j) sc[j] = sxs[wm * 64 + 16 * j + r] * wsc;
+    }
   };
   auto fold = [&](f32x4 (&dst)[4], const f32x4 (&p)[4], const float (&s)[4]) {
 #pragma unroll
@@ -177,11 +187,18 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
     for (int i = 0; i < 8; ++i) {
       if (i < 5 && kb + 1 < a.KB) issue_part(st ^ 1, kb + 1, i);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 4; ++j) {
         // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
-        pr[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
-                                                                0, 127);
-      asm volatile("" ::"v"(pr[0]), "v"(pr[1]), "v"(pr[2]), "v"(pr[3]) : "memory");
+        if constexpr (BLOCK)
+          pr[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0, 127,
+                                                                  0, 127);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], acc[i][j], 0, 0, 0, 127, 0, 127);
+      }
+      if constexpr (BLOCK)
+        asm volatile("" ::"v"(pr[0]), "v"(pr[1]), "v"(pr[2]), "v"(pr[3]) : "memory");
+      else
+        asm volatile("" ::"v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]) : "memory");
       if (i < 7) {
         af = frag(sa, wn * 128 + 16 * (i + 1) + r);
       } else {
@@ -190,9 +207,11 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
         LQ_WAIT_VM0();
         __builtin_amdgcn_s_barrier();
       }
-      asm volatile("" ::: "memory");
-      fold(acc[i], pr, sc);
-      asm volatile("" ::"v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]));
+      if constexpr (BLOCK) {
+        asm volatile("" ::: "memory");
+        fold(acc[i], pr, sc);
+        asm volatile("" ::"v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]));
+      }
     }
     if (kb + 1 < a.KB) block_start(st ^ 1, kb + 1);
   }
@@ -206,9 +225,21 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
     for (int i = 0; i < 8; ++i) {
       const int n = n0 + wn * 128 + 16 * i + 4 * t;
       if (n >= a.N) continue;
-      uint16_t* dst = a.y + static_cast<size_t>(m) * a.ldy + n;
-      *reinterpret_cast<u32x2*>(dst) = u32x2{f32_to_bf16(acc[i][j][0]) | (uint32_t(f32_to_bf16(acc[i][j][1])) << 16),
-                                             f32_to_bf16(acc[i][j][2]) | (uint32_t(f32_to_bf16(acc[i][j][3])) << 16)};
+      f32x4 v = acc[i][j];
+      if constexpr (!BLOCK) v = f32x4{v[0] * a.alpha, v[1] * a.alpha, v[2] * a.alpha, v[3] * a.alpha};
+      const size_t o = static_cast<size_t>(m) * a.ldy + n;
+      if constexpr (OUT == kOutBf16) {
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.y) + o) =
+            u32x2{f32_to_bf16(v[0]) | (uint32_t(f32_to_bf16(v[1])) << 16),
+                  f32_to_bf16(v[2]) | (uint32_t(f32_to_bf16(v[3])) << 16)};
+      } else {
+        f32x4* dst = reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + o);
+        if constexpr (OUT == kOutF32Acc) {
+          const f32x4 old = *dst;
+          v = f32x4{old[0] + v[0], old[1] + v[1], old[2] + v[2], old[3] + v[3]};
+        }
+        *dst = v;
+      }
     }
   }
 }
@@ -236,6 +267,51 @@ __global__ void __launch_bounds__(256) quant_fp8_g128_kernel(const uint16_t* __r
   if (lane == 0) scale[static_cast<size_t>(m) * KB + kb] = s;
 }
 
+// Per-tensor FP8 activation quantizer (reference src/core/prefill_gemm.cu:496-511): each value rounded to BF16
+// first (production's activations are BF16), times 1 / input_scale, then E4M3 with saturation to +-448 (NaN
+// stays NaN). Four values per thread.
+__global__ void __launch_bounds__(256) quant_fp8_pt_kernel(const float* __restrict__ x, size_t quads, float inv_scale,
+                                                           uint8_t* __restrict__ q) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(256) + threadIdx.x; i < quads; i += static_cast<size_t>(gridDim.x) * 256) {
+    const f32x4 f = reinterpret_cast<const f32x4*>(x)[i];
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float b = bf16_to_f32(f32_to_bf16(f[k])) * inv_scale;
+      v[k] = isnan(b) ? b : fminf(fmaxf(b, -448.f), 448.f);
+    }
+    const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+    const uint32_t w = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], lo, true);
+    reinterpret_cast<uint32_t*>(q)[i] = w;
+  }
+}
+
+template <bool BLOCK, int OUT>
+int prefill_launch(PrefillArgs a, const char* name, hipStream_t s) {
+  const std::string nm(name);
+  if (a.N <= 0 || a.K <= 0 || a.N % 128 != 0 || a.K % 128 != 0)
+    return fail(LQ_ERR_SHAPE, "prefill_gemm: N % 128 and K % 128 must be 0");
+  if (a.M < 1) return LQ_OK;  // nothing to do (the reference returns silently)
+  if (a.ldy < a.N || a.ldy % 4 != 0) return fail(LQ_ERR_SHAPE, nm + ": ldy must be >= N and a multiple of 4");
+  // operand byte offsets are 32-bit
+  if (static_cast<long long>(a.N) * a.K >= (1LL << 31) || static_cast<long long>(a.M) * a.K >= (1LL << 31))
+    return fail(LQ_ERR_SHAPE, nm + ": N * K and M * K must be below 2^31");
+  if (!a.xq || !a.w || !a.y || (BLOCK && (!a.xs || !a.ws))) return fail(LQ_ERR_ARG, nm + ": null pointer");
+  if (reinterpret_cast<uintptr_t>(a.y) % (OUT == kOutBf16 ? 8 : 16) != 0)
+    return fail(LQ_ERR_ARG, nm + ": y must be 8-byte (BF16) or 16-byte (FP32) aligned");
+  a.KB = a.K / 128;
+  a.tiles_m = cdiv(a.M, kBM);
+  a.tiles_n = cdiv(a.N, kBN);
+  const long long blocks = static_cast<long long>(a.tiles_m) * a.tiles_n;
+  // 130 KB of dynamic LDS is above the default per-launch limit; raise it (once per instantiation).
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_fp8_kernel<BLOCK, OUT>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStage);
+  if (attr != hipSuccess) return fail(LQ_ERR_LAUNCH, nm + ": " + hipGetErrorString(attr));
+  hipLaunchKernelGGL((prefill_fp8_kernel<BLOCK, OUT>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 2 * kStage,
+                     s, a);
+  return check_launch(name);
+}
+
 }  // namespace
 }  // namespace lq
 
@@ -254,14 +330,6 @@ int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* sc
 
 int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws, uint16_t* y,
                          int ldy, int N, int K, void* stream) {
-  if (N <= 0 || K <= 0 || N % 128 != 0 || K % 128 != 0)
-    return fail(LQ_ERR_SHAPE, "prefill_gemm: N % 128 and K % 128 must be 0");
-  if (M < 1) return LQ_OK;  // nothing to do (the reference returns silently)
-  if (ldy < N || ldy % 4 != 0) return fail(LQ_ERR_SHAPE, "prefill_gemm: ldy must be >= N and a multiple of 4");
-  // operand byte offsets are 32-bit
-  if (static_cast<long long>(N) * K >= (1LL << 31) || static_cast<long long>(M) * K >= (1LL << 31))
-    return fail(LQ_ERR_SHAPE, "prefill_gemm: N * K and M * K must be below 2^31");
-  if (!xq || !xs || !w || !ws || !y) return fail(LQ_ERR_ARG, "prefill_gemm: null pointer");
   PrefillArgs a{};
   a.xq = xq;
   a.xs = xs;
@@ -272,18 +340,49 @@ int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_
   a.M = M;
   a.N = N;
   a.K = K;
-  a.KB = K / 128;
-  a.tiles_m = cdiv(M, kBM);
-  a.tiles_n = cdiv(N, kBN);
-  const long long blocks = static_cast<long long>(a.tiles_m) * a.tiles_n;
-  // 130 KB of dynamic LDS is above the default per-launch limit; raise it (idempotent, per process).
-  static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_fp8_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                          2 * kStage);
-  if (attr != hipSuccess) return fail(LQ_ERR_LAUNCH, std::string("prefill_gemm: ") + hipGetErrorString(attr));
-  hipLaunchKernelGGL(prefill_fp8_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 2 * kStage,
-                     static_cast<hipStream_t>(stream), a);
-  return check_launch("prefill_gemm");
+  return prefill_launch<true, kOutBf16>(a, "prefill_gemm", static_cast<hipStream_t>(stream));
+}
+
+int lq_quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q, void* stream) {
+  if (M < 1 || K <= 0 || K % 4 != 0) return fail(LQ_ERR_SHAPE, "quant_act_fp8: M >= 1 and K % 4 == 0");
+  if (!x || !q) return fail(LQ_ERR_ARG, "quant_act_fp8: null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q) % 4 != 0)
+    return fail(LQ_ERR_ARG, "quant_act_fp8: x must be 16-byte and q 4-byte aligned");
+  const size_t quads = static_cast<size_t>(M) * K / 4;
+  const unsigned grid = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 256 * 64));
+  hipLaunchKernelGGL(quant_fp8_pt_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), x, quads,
+                     1.f / input_scale, q);
+  return check_launch("quant_act_fp8");
+}
+
+int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
+                        int accumulate, void* stream) {
+  PrefillArgs a{};
+  a.xq = xq;
+  a.w = w;
+  a.alpha = alpha;
+  a.y = y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  return accumulate ? prefill_launch<false, kOutF32Acc>(a, "prefill_gemm_fp8", s)
+                    : prefill_launch<false, kOutF32>(a, "prefill_gemm_fp8", s);
+}
+
+int lq_prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, float alpha, uint16_t* y, int ldy, int N,
+                                int K, void* stream) {
+  PrefillArgs a{};
+  a.xq = xq;
+  a.w = w;
+  a.alpha = alpha;
+  a.y = y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  return prefill_launch<false, kOutBf16>(a, "prefill_gemm_fp8_bf16out", static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -671,6 +671,48 @@ __global__ void __launch_bounds__(256) half_rows_kernel(const void* __restrict__
   if (blockIdx.y == 0 && threadIdx.x == 0) xinv[m] = ldexpf(1.f, e - 15);
 }
 
+// RMSNorm of each row into FP32 `out` and the FP16 row copy the stream GEMM reads (reference
+// src/core/stream_gemm.cu:380-418): rstd = 1 / sqrt(sum(x^2) / H + eps), v = x * rstd * w' with w' = 1 + w
+// (Gemma) or w, then xh = f16_rn(v * 2^(15 - e)), xinv = 2^(e - 15) from the row's largest |v| (the values
+// to_half_rows makes from `out`). One block per row; the FP16 pass recomputes v exactly as the first pass did.
+__global__ void __launch_bounds__(256) rmsnorm_half_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                           float* __restrict__ out, _Float16* __restrict__ xh,
+                                                           float* __restrict__ xinv, int H, float eps, bool gemma) {
+  __shared__ float red[4];
+  const size_t r = blockIdx.x;
+  const float* row = x + r * H;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  float ss = 0.f;
+  for (int h = tid; h < H; h += 256) ss += row[h] * row[h];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rstd = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+  auto val = [&](int h) {
+    const float wf = bf16_to_f32(w[h]);
+    return row[h] * rstd * (gemma ? 1.f + wf : wf);
+  };
+  float mx = 0.f;
+  for (int h = tid; h < H; h += 256) {
+    const float v = val(h);
+    out[r * H + h] = v;
+    mx = fmaxf(mx, fabsf(v));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  __syncthreads();
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.f && isfinite(mx)) frexpf(mx, &e);
+  const float sc = ldexpf(1.f, 15 - e);
+  for (int h = tid; h < H; h += 256) xh[r * H + h] = static_cast<_Float16>(val(h) * sc);
+  if (tid == 0) xinv[r] = ldexpf(1.f, e - 15);
+}
+
 // ---------------- host side ----------------
 
 struct Mat {
@@ -814,6 +856,15 @@ int lq_to_half_rows(const float* x, int M, int K, uint16_t* xh, float* xinv, voi
 
 int lq_bf16_to_half_rows(const uint16_t* x, int M, int K, uint16_t* xh, float* xinv, void* stream) {
   return half_rows(true, x, M, K, xh, xinv, static_cast<hipStream_t>(stream));
+}
+
+int lq_rmsnorm_half(const float* x, const uint16_t* w, float* out, uint16_t* xh, float* xinv, int rows, int H, float eps,
+                    int gemma, void* stream) {
+  if (rows < 1 || H < 1) return fail(LQ_ERR_SHAPE, "rmsnorm_half: rows and H must be positive");
+  if (!x || !w || !out || !xh || !xinv) return fail(LQ_ERR_ARG, "rmsnorm_half: null pointer");
+  hipLaunchKernelGGL(rmsnorm_half_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), x, w, out,
+                     reinterpret_cast<_Float16*>(xh), xinv, H, eps, gemma != 0);
+  return check_launch("rmsnorm_half");
 }
 
 int lq_stream_gemm_fp8(const uint16_t* xh, const float* xinv, int M, const uint8_t* w, float wscale, float* y, int N,

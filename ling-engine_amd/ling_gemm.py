@@ -43,6 +43,10 @@ SIGNATURES = {
     "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_quant_act_fp8_g128": (_I, [_P, _I, _I, _P, _P, _P]),
     "lq_prefill_fp8_block": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
+    "lq_rmsnorm_half": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _I, _P]),
+    "lq_quant_act_fp8": (_I, [_P, _I, _I, _F, _P, _P]),
+    "lq_prefill_gemm_fp8": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _I, _P]),
+    "lq_prefill_gemm_fp8_bf16out": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _P]),
 }
 
 
@@ -191,6 +195,17 @@ def bf16_to_half_rows(x: torch.Tensor):
     return xh, xinv
 
 
+def rmsnorm_half(x, w, eps: float, gemma: bool = True):
+    """x FP32 [rows][H], w BF16 [H] -> (out FP32, xh FP16, xinv FP32 [rows])."""
+    rows, H = x.shape
+    out = torch.empty_like(x, dtype=torch.float32)
+    xh = torch.empty((rows, H), dtype=torch.float16, device=x.device)
+    xinv = torch.empty(rows, dtype=torch.float32, device=x.device)
+    _check(lib.lq_rmsnorm_half(_ptr(_dev(x, torch.float32)), _ptr(_dev(w, torch.bfloat16)), _ptr(out), _ptr(xh),
+                               _ptr(xinv), rows, H, eps, int(gemma), _stream()))
+    return out, xh, xinv
+
+
 def stream_gemm_fp8(xh, xinv, w, wscale: float, N: int, K: int, y=None):
     M = xh.shape[0]
     y = torch.empty((M, N), dtype=torch.float32, device=xh.device) if y is None else y
@@ -265,4 +280,29 @@ def prefill_fp8_block(xq, xs, w, ws, N: int, y=None, ldy: int | None = None):
     y = torch.empty((M, ldy), dtype=torch.bfloat16, device=xq.device) if y is None else y
     _check(lib.lq_prefill_fp8_block(_ptr(_dev(xq, torch.uint8)), _ptr(_dev(xs, torch.float32)), M, _ptr(w),
                                     _ptr(_dev(ws, torch.float32)), _ptr(y), ldy, N, K, _stream()))
+    return y
+
+
+def quant_act_fp8(x, input_scale: float):
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    _check(lib.lq_quant_act_fp8(_ptr(_dev(x, torch.float32)), M, K, input_scale, _ptr(q), _stream()))
+    return q
+
+
+def prefill_gemm_fp8(xq, w, alpha: float, N: int, y=None, ldy: int | None = None, accumulate: bool = False):
+    M, K = xq.shape
+    ldy = N if ldy is None else ldy
+    y = torch.empty((M, ldy), dtype=torch.float32, device=xq.device) if y is None else y
+    _check(lib.lq_prefill_gemm_fp8(_ptr(_dev(xq, torch.uint8)), M, _ptr(w), alpha, _ptr(_dev(y, torch.float32)), ldy, N,
+                                   K, int(accumulate), _stream()))
+    return y
+
+
+def prefill_gemm_fp8_bf16out(xq, w, alpha: float, N: int, y=None, ldy: int | None = None):
+    M, K = xq.shape
+    ldy = N if ldy is None else ldy
+    y = torch.empty((M, ldy), dtype=torch.bfloat16, device=xq.device) if y is None else y
+    _check(lib.lq_prefill_gemm_fp8_bf16out(_ptr(_dev(xq, torch.uint8)), M, _ptr(w), alpha,
+                                           _ptr(_dev(y, torch.bfloat16)), ldy, N, K, _stream()))
     return y

@@ -408,6 +408,30 @@ void or_to_half_rows(const float* x, int M, int K, uint16_t* xh, float* xinv) {
   }
 }
 
+/* RMSNorm + FP16 row copy (stream_gemm.cu:380-418): the sum of squares in double (any FP32 order of the
+ * device is within its rounding of this), rstd = 1 / sqrtf(float(sum / H) + eps), v = x * rstd * w' in FP32
+ * (w' = 1 + w for Gemma), then the to_half_rows conversion of v. */
+void or_rmsnorm_half(const float* x, const uint16_t* w, int rows, int H, float eps, int gemma, float* out,
+                     uint16_t* xh, float* xinv) {
+  for (int r = 0; r < rows; ++r) {
+    const float* row = x + (size_t)r * H;
+    double ss = 0.0;
+    for (int h = 0; h < H; ++h) ss += (double)row[h] * row[h];
+    const float rstd = 1.f / sqrtf((float)(ss / H) + eps);
+    for (int h = 0; h < H; ++h) {
+      const float wf = or_bf16_float(w[h]);
+      out[(size_t)r * H + h] = row[h] * rstd * (gemma ? 1.f + wf : wf);
+    }
+  }
+  or_to_half_rows(out, rows, H, xh, xinv);
+}
+
+/* Per-tensor FP8 activation quantizer (prefill_gemm.cu:496-511): E4M3_satfinite(bf16(x) * (1 / input_scale)). */
+void or_quant_act_fp8(const float* x, size_t n, float input_scale, uint8_t* q) {
+  const float inv = 1.f / input_scale;
+  for (size_t i = 0; i < n; ++i) q[i] = or_e4m3_encode(or_bf16_float(or_bf16_bits(x[i])) * inv);
+}
+
 /* ------------------------------------------------------------------------------------------------ */
 /* reference GEMM                                                                                     */
 /* ------------------------------------------------------------------------------------------------ */

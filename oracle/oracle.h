@@ -110,6 +110,12 @@ void or_stream_fp8_pc_bf16(const uint16_t* x, int M, const uint8_t* q, const flo
 void or_prefill_fp8_rows(const uint8_t* xq, const float* xs, const int* rows, int R, const uint8_t* wq,
                          const float* ws, int N, int K, float* y, int threads);
 
+/* RMSNorm rows (FP32 out) and their FP16 copy with row scales, as rmsnorm_half makes them. */
+void or_rmsnorm_half(const float* x, const uint16_t* w, int rows, int H, float eps, int gemma, float* out,
+                     uint16_t* xh, float* xinv);
+/* Per-tensor FP8 activations: E4M3_satfinite(bf16(x) * (1 / input_scale)). */
+void or_quant_act_fp8(const float* x, size_t n, float input_scale, uint8_t* q);
+
 int or_hardware_threads(void);
 
 #ifdef __cplusplus

@@ -61,6 +61,8 @@ def _load():
         "or_epi_residual_bf16": (None, [P, P, sz, P]),
         "or_stream_fp8_pc_bf16": (None, [P, i, P, P, i, i, i, i, P, i]),
         "or_prefill_fp8_rows": (None, [P, P, P, i, P, P, i, i, P, i]),
+        "or_rmsnorm_half": (None, [P, P, i, i, f, i, P, P, P]),
+        "or_quant_act_fp8": (None, [P, sz, f, P]),
         "or_hardware_threads": (i, []),
     }
     for name, (res, args) in sig.items():
@@ -262,6 +264,24 @@ def prefill_fp8_rows(xq, xs, rows, wq, ws, threads: int = 0) -> np.ndarray:
                             _p(np.ascontiguousarray(wq)), _p(np.ascontiguousarray(ws, np.float32)), N, K, _p(y),
                             threads)
     return y
+
+
+def rmsnorm_half(x: np.ndarray, w_bf16: np.ndarray, eps: float, gemma: bool = True):
+    x = np.ascontiguousarray(x, np.float32)
+    rows, H = x.shape
+    out = np.empty_like(x)
+    xh = np.empty((rows, H), np.uint16)
+    xinv = np.empty(rows, np.float32)
+    lib.or_rmsnorm_half(_p(x), _p(np.ascontiguousarray(w_bf16, np.uint16)), rows, H, eps, int(gemma),
+                        _p(out), _p(xh), _p(xinv))
+    return out, xh, xinv
+
+
+def quant_act_fp8(x: np.ndarray, input_scale: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.shape, np.uint8)
+    lib.or_quant_act_fp8(_p(x), x.size, input_scale, _p(q))
+    return q
 
 
 def hardware_threads() -> int:

@@ -119,3 +119,89 @@ def test_prefill_errors(L):
     xs = torch.ones((4, 1), dtype=torch.float32, device=DEV)
     with pytest.raises(L.LingGemmError, match="N % 128 and K % 128 must be 0"):
         L.prefill_fp8_block(xq, xs, torch.zeros(64 * 128, dtype=torch.uint8, device=DEV), xs, 64)
+
+
+# ---------------- per-tensor forms (reference prefill_gemm_fp8 / _bf16out / quant_act_fp8) ----------------
+def test_quant_act_fp8_per_tensor_bit_exact(L):
+    x = O.normal_f32(61, 3.0, (37, 512))
+    x[0, :4] = [0.0, -0.0, 1e6, -1e6]  # zeros and saturation
+    q = L.quant_act_fp8(to_dev(x), 0.0123)
+    assert np.array_equal(q.cpu().numpy(), O.quant_act_fp8(x, 0.0123))
+
+
+def pt_case(L, M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    wq = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    wq[(wq & 0x7F) == 0x7F] = 0x38
+    xq = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    xq[(xq & 0x7F) == 0x7F] = 0x38
+    return wq, xq, L.retile_fp8(to_dev(wq))
+
+
+E4M3 = np.array([O.lib.or_e4m3_decode(c) for c in range(256)], np.float64)
+
+
+def pt_ref(xq, wq, alpha, rows=None):
+    """Exact (float64) alpha * xq . wq^T on the given rows, and alpha * |xq| . |wq|^T (the size of the terms)."""
+    rows = np.arange(xq.shape[0]) if rows is None else rows
+    xd, wd = E4M3[xq[rows]], E4M3[wq]
+    return alpha * (xd @ wd.T), abs(alpha) * (np.abs(xd) @ np.abs(wd).T)
+
+
+def check_f32(got, ref_abs, what, base=None):
+    """FP32 outputs: max |err| / max(|ref|, rms(row)) <= 2e-3. The bound is the FP8 MFMA's: it sums a 128-value
+    block's products at reduced precision (measured about 6e-5 of the sum of the terms' magnitudes, a few 1e-4
+    of the row's rms), well inside the 1e-2 of the BF16 outputs."""
+    ref = ref_abs[0] if base is None else ref_abs[0] + base
+    rms = np.sqrt(np.mean(ref * ref, axis=-1, keepdims=True)) + 1e-30
+    rel = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms))
+    assert rel <= 2e-3, f"{what}: max rel {rel:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (200, 384, 640), (513, 256, 1024)])
+def test_prefill_per_tensor_f32_and_accumulate(L, M, N, K):
+    wq, xq, tw = pt_case(L, M, N, K, 70 + M)
+    alpha = 3.0e-4
+    y = L.prefill_gemm_fp8(to_dev(xq), tw, alpha, N)
+    ref = pt_ref(xq, wq, alpha)
+    check_f32(y.cpu().numpy().astype(np.float64), ref, f"per-tensor M={M}")
+    base = O.normal_f32(M, 1.0, (M, N))
+    y2 = torch.from_numpy(base).to(DEV)
+    L.prefill_gemm_fp8(to_dev(xq), tw, alpha, N, y=y2, accumulate=True)
+    check_f32(y2.cpu().numpy().astype(np.float64), ref, f"accumulate M={M}", base=base.astype(np.float64))
+
+
+def test_prefill_per_tensor_bf16out_and_ldy(L):
+    M, N, K = 90, 256, 512
+    wq, xq, tw = pt_case(L, M, N, K, 5)
+    ldy = N + 32
+    raw = pt_ref(xq, wq, 1.0)[0]
+    alpha = float(1.0 / np.sqrt(np.mean(raw * raw)))  # outputs of unit size, as the BF16 bounds assume
+    y = torch.full((M, ldy), 5.0, dtype=torch.bfloat16, device=DEV)
+    L.prefill_gemm_fp8_bf16out(to_dev(xq), tw, alpha, N, y=y, ldy=ldy)
+    assert np.all(y[:, N:].float().cpu().numpy() == 5.0)
+    check(bf16_host(y[:, :N].contiguous()), (alpha * raw).astype(np.float32), "bf16out")
+
+
+def test_prefill_per_tensor_config4_rows(L):
+    """Config-4 gate|up shape through the per-tensor form, checked on every 128th row."""
+    M, N, K = 4096, 34816, 5120
+    wq, xq, tw = pt_case(L, M, N, K, 9)
+    y = L.prefill_gemm_fp8(to_dev(xq), tw, 2e-4, N)
+    rows = np.arange(0, M, 128)
+    check_f32(y.cpu().numpy()[rows].astype(np.float64), pt_ref(xq, wq, 2e-4, rows), "per-tensor config4")
+
+
+# ---------------- rmsnorm_half (reference stream_gemm.cu:380-418) ----------------
+@pytest.mark.parametrize("rows,H,gemma", [(1, 5120, True), (17, 5120, True), (3, 17408, False), (68, 1024, True)])
+def test_rmsnorm_half(L, rows, H, gemma):
+    x = O.normal_f32(80 + rows, 2.0, (rows, H))
+    w = O.normal_bf16(81 + rows, 0.1, (H,))
+    out, xh, xinv = L.rmsnorm_half(to_dev(x), bf16_dev(w), 1e-6, gemma)
+    ro, _, _ = O.rmsnorm_half(x, w, 1e-6, gemma)
+    o = out.cpu().numpy()
+    assert np.max(np.abs(o - ro) / (np.abs(ro) + 1e-6 * np.abs(ro).max())) <= 1e-5
+    # the FP16 copy is exactly to_half_rows of the device's own FP32 output
+    ch, ci = O.to_half_rows(o)
+    assert np.array_equal(xh.view(torch.int16).cpu().numpy().view(np.uint16), ch)
+    assert np.array_equal(xinv.cpu().numpy(), ci)

@@ -271,3 +271,26 @@ def test_generator_is_portable():
     assert np.array_equal(a, b)
     big = O.normal_f32(123, 1.0, 200000)
     assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+
+
+def test_rmsnorm_half_vs_float64():
+    x = O.normal_f32(91, 1.5, (4, 2048))
+    w = O.normal_bf16(92, 0.1, (2048,))
+    for gemma in (True, False):
+        out, xh, xinv = O.rmsnorm_half(x, w, 1e-6, gemma)
+        wf = O.bf16_to_f32(w).astype(np.float64)
+        ref = x / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * ((1 + wf) if gemma else wf)
+        assert np.max(np.abs(out - ref)) <= 1e-6 * np.abs(ref).max()
+        h2, i2 = O.to_half_rows(out)
+        assert np.array_equal(xh, h2) and np.array_equal(xinv, i2)
+
+
+def test_quant_act_fp8_per_tensor_vs_torch():
+    import torch
+    x = O.normal_f32(93, 4.0, (8, 512))
+    x[0, :3] = [1e9, -1e9, 0.0]
+    s = 0.0123
+    q = O.quant_act_fp8(x, s)
+    xb = torch.from_numpy(x).to(torch.bfloat16).float() * (1.0 / np.float32(s))
+    ref = xb.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(q, ref)
