@@ -35,6 +35,7 @@
 #include "lq_workspace.hpp"
 
 #include <algorithm>
+#include <cstddef>
 #include <cstdlib>
 #include <cstring>
 #include <string>
@@ -44,19 +45,24 @@ namespace {
 
 constexpr int kWaves = 4;  // waves per workgroup, one per tile slot of the tile group
 constexpr int kThreads = kWaves * kWave;
-// 16-row tiles per wave: one, or one gate and one up tile with the SiLU*mul epilogue. A tile group is the
-// workgroup's 4 waves' tiles: 64 output rows.
-template <bool PAIR>
-constexpr int tiles_per_wave() { return PAIR ? 2 : 1; }
-constexpr int kGroupRows = 64;  // output rows (columns of y) per tile group
 constexpr int kMaxMats = 4;
-
 
 enum WFmt { kFp8 = 0, kFp4 = 1, kFp4Coded = 2 };
 
+// 16-row tiles per wave: one gate and one up tile with the SiLU*mul epilogue; two FP8 tiles; four NVFP4 tiles
+// (half the bytes per tile and chunk). Enough weight bytes per load stage keep the HBM stream deep, and every
+// activation operand read from LDS feeds T MFMAs. Fixed per format (never chosen by M: row invariance).
+__host__ __device__ constexpr int tiles_per_wave(int wf, bool pair) { return pair ? 2 : wf == kFp8 ? 2 : 4; }
+// Output rows (columns of y) per tile group: the workgroup's 4 waves' tiles (gate rows only for a pair).
+__host__ __device__ constexpr int group_rows(int wf, bool pair) {
+  return 16 * 4 * (pair ? tiles_per_wave(wf, pair) / 2 : tiles_per_wave(wf, pair));
+}
+
 // Weight chunks in flight per wave (the computed one included), by register budget.
 template <int T>
-__host__ __device__ constexpr int pf_stages(int G) { return T == 1 ? (G <= 2 ? 8 : G <= 4 ? 6 : 4) : (G <= 2 ? 6 : 4); }
+__host__ __device__ constexpr int pf_stages(int G) {
+  return T == 2 ? (G <= 1 ? 8 : G <= 2 ? 6 : 4) : (G <= 1 ? 6 : G <= 2 ? 4 : G <= 3 ? 3 : 2);
+}
 
 struct StreamArgs {
   const void* x;      // [M][K] BF16 or FP16
@@ -77,7 +83,25 @@ struct StreamArgs {
   int ldy[kMaxMats];
   float* partials;  // [2 * P][T * G * 4][256] per workgroup slot
   int* counters;    // [TG]
+  unsigned long long* trace;  // [P][16] s_memrealtime stamps per workgroup (LQ_STREAM_TRACE builds), or null
 };
+
+// The kernel touches one field per 64-byte line of its arguments at entry (see stream_kernel).
+static_assert(sizeof(StreamArgs) <= 320 && offsetof(StreamArgs, x) / 64 == 0 &&
+                  (offsetof(StreamArgs, w) + 2 * sizeof(void*)) / 64 == 1 &&
+                  (offsetof(StreamArgs, svec) + 2 * sizeof(void*)) / 64 == 2 && offsetof(StreamArgs, resid) / 64 == 3 &&
+                  (offsetof(StreamArgs, tg0) + 4 * sizeof(int)) / 64 == 4,
+              "argument lines touched at kernel entry");
+
+// Phase stamps of a workgroup for builds with LQ_STREAM_TRACE: kept in registers, written once at exit.
+// 0 entry, 1 first chunk computed, 2 stream done, 3 partials published, 4 arrival counted, 5 reduced, 6 exit,
+// 7 prologue loads issued, 8 first partial added, 9 reduction loop done, 10 arguments read, 11 tiles set up,
+// 12 / 13 first / last epilogue inputs issued, 14 first ring stage issued.
+#ifdef LQ_STREAM_TRACE
+#define LQ_TS(i) (ts[i] = __builtin_amdgcn_s_memrealtime())
+#else
+#define LQ_TS(i) ((void)0)
+#endif
 
 // One chunk of weights for the lane: FP8 32 bytes (two pieces) per tile; NVFP4 16 bytes + 2 scales.
 template <int WF, int T>
@@ -146,16 +170,16 @@ __device__ __forceinline__ u32x4 a_operand(const WRegs<WF, T>& R, int i, int s, 
 // LDS image of one chunk of activations: row m's 16 units of 16 bytes (8 values), unit u at (u ^ (m & 15)).
 __device__ __forceinline__ int xs_off(int row, int unit) { return row * 256 + ((unit ^ (row & 15)) << 4); }
 
-// Accumulators are split by MFMA step parity (two independent chains per output tile and row group), so
-// consecutive MFMAs never wait on each other's results; the two halves are added once per segment.
+// One accumulator chain per output tile and row group: a step's T x G MFMAs (T >= 2) are independent of each
+// other, which covers the MFMA result latency.
 template <int WF, bool F16, int G, int T>
-__device__ __forceinline__ void mfma_step(const WRegs<WF, T>& R, int s, const u32x4 (&b)[G], f32x4 (&acc)[2][T][G],
+__device__ __forceinline__ void mfma_step(const WRegs<WF, T>& R, int s, const u32x4 (&b)[G], f32x4 (&acc)[T][G],
                                           const uint8_t* const (&tab)[T]) {
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const u32x4 a = a_operand<WF, F16, T>(R, i, s, tab[i]);
 #pragma unroll
-    for (int g = 0; g < G; ++g) acc[s & 1][i][g] = mfma16x16x32(a, b[g], acc[s & 1][i][g], F16);
+    for (int g = 0; g < G; ++g) acc[i][g] = mfma16x16x32(a, b[g], acc[i][g], F16);
   }
 }
 
@@ -167,7 +191,7 @@ __device__ __forceinline__ void read_b(u32x4 (&b)[G], const uint8_t* xs, int s, 
 
 // One chunk with the activation operands read from LDS inside (the next step's while the current computes).
 template <int WF, bool F16, int G, int T>
-__device__ __forceinline__ void compute_lds(const WRegs<WF, T>& R, const uint8_t* xs, f32x4 (&acc)[2][T][G], int r,
+__device__ __forceinline__ void compute_lds(const WRegs<WF, T>& R, const uint8_t* xs, f32x4 (&acc)[T][G], int r,
                                             int t, const uint8_t* const (&tab)[T]) {
   u32x4 b[2][G];
   read_b<G>(b[0], xs, 0, r, t);
@@ -198,7 +222,7 @@ __device__ __forceinline__ int epi_row(int wtile0, int i, int t) {
   return (wtile0 + (PAIR ? i % (T / 2) : i)) * 16 + 4 * t;
 }
 
-template <int G, bool PAIR, bool OUTF32, int T = tiles_per_wave<PAIR>()>
+template <int G, bool PAIR, bool OUTF32, int T>
 __device__ __forceinline__ void epi_load(const StreamArgs& a, int mi, int wtile0, EpiIn<G, T>& e, int r, int t) {
 #pragma unroll
   for (int i = 0; i < T; ++i) {
@@ -225,7 +249,7 @@ __device__ __forceinline__ void epi_load(const StreamArgs& a, int mi, int wtile0
 }
 
 // Epilogue of one lane's outputs: acc[i][g][v] is row 16 * tile(i) + 4t + v, token 16g + r.
-template <int G, bool PAIR, bool OUTF32, int T = tiles_per_wave<PAIR>()>
+template <int G, bool PAIR, bool OUTF32, int T>
 __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0, const f32x4 (&acc)[T][G],
                                          const EpiIn<G, T>& e, int r, int t) {
 #pragma unroll
@@ -298,7 +322,7 @@ __device__ __forceinline__ void seg_tiles(const StreamArgs& a, int tg, int wave,
     while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
   }
   s.mi = mi;
-  s.wtile0 = (tg - a.tg0[mi]) * (kGroupRows / 16) + wave * (PAIR ? T / 2 : T);
+  s.wtile0 = (tg - a.tg0[mi]) * (group_rows(WF, PAIR) / 16) + wave * (PAIR ? T / 2 : T);
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
@@ -336,65 +360,47 @@ __device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
   return s;
 }
 
-// The finishing step of split tile groups: the last workgroup to arrive adds every workgroup's partial in
-// workgroup order. Both of the range's tile groups (first, last) are reduced together, QB partials of each
-// in flight at a time: loads may complete in any order, the adds are in order.
+// The finishing step of a split tile group: the last workgroup to arrive adds every workgroup's partial in
+// workgroup order. Every workgroup (the finisher included) published its partial before arriving, so all of
+// them are read back from memory, D partials per batch: a batch's loads are all issued before its adds, so a
+// fan-in of up to D costs one memory round trip.
 template <int G, int T>
-__device__ __forceinline__ void reduce_partials(const StreamArgs& a, int p, const bool (&doit)[2],
-                                                const SplitInfo (&si)[2], f32x4 (&accF)[T][G], f32x4 (&accL)[T][G],
-                                                int r) {
+__device__ __forceinline__ void reduce_partials(const StreamArgs& a, const SplitInfo& si, f32x4 (&acc)[T][G], int r,
+                                                unsigned long long (&ts)[16]) {
   constexpr int NV = T * G;  // accumulator vectors per thread
-  constexpr int QB = NV <= 2 ? 4 : 2;
+  constexpr int D = NV <= 4 ? 8 : NV <= 8 ? 4 : NV <= 10 ? 3 : NV <= 16 ? 2 : 1;
   const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
-  const int n[2] = {doit[0] ? si[0].pl - si[0].pf + 1 : 0, doit[1] ? si[1].pl - si[1].pf + 1 : 0};
-  const int nmax = max(n[0], n[1]);
+  const int n = si.pl - si.pf + 1;
   // rows past M read nothing (an out-of-range offset returns zeros): they only reach outputs never stored
   unsigned rowmask[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) rowmask[g] = 16 * g + r < a.M ? 0u : 0x80000000u;
-  f32x4 own[2][T][G];
+  f32x4 ring[D][NV];
+  // Only positions that exist are loaded (out-of-range buffer loads are not free: a burst of them delays the
+  // wanted ones).
+  auto issue = [&](int k, int b) {
+    if (k >= n) return;
+    const int off = slot_off<G, T>(si.pf + k, (k > 0 || si.pf_first) ? 0 : 1);
 #pragma unroll
-  for (int i = 0; i < T; ++i)
+    for (int i = 0; i < T; ++i)
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      own[0][i][g] = accF[i][g];
-      own[1][i][g] = accL[i][g];
-    }
-  for (int q0 = 0; q0 < nmax; q0 += QB) {
-    // Unconditional loads: a position past a group's count, or this workgroup's own partial (kept in
-    // registers), reads nothing.
-    f32x4 pv[2][QB][NV];
+      for (int g = 0; g < G; ++g)
+        ring[b][i * G + g] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       prs, static_cast<int>((off + (i * G + g) * 16 * kThreads) | rowmask[g]), 0, kSc1));
+  };
+  for (int q0 = 0; q0 < n; q0 += D) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int b = 0; b < D; ++b) issue(q0 + b, b);
 #pragma unroll
-      for (int b = 0; b < QB; ++b) {
-        const int k = q0 + b, q = si[h].pf + k;
-        const unsigned skip = (k < n[h] && q != p) ? 0u : 0x80000000u;
-        const int off = slot_off<G, T>(q, (k > 0 || si[h].pf_first) ? 0 : 1);
-#pragma unroll
-        for (int i = 0; i < T; ++i)
-#pragma unroll
-          for (int g = 0; g < G; ++g)
-            pv[h][b][i * G + g] = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           prs, static_cast<int>((off + (i * G + g) * 16 * kThreads) | skip | rowmask[g]), 0, kSc1));
-      }
-#pragma unroll
-    for (int b = 0; b < QB; ++b) {
+    for (int b = 0; b < D; ++b) {
       const int k = q0 + b;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bool mine = si[h].pf + k == p;
+      if (k < n) {
 #pragma unroll
         for (int i = 0; i < T; ++i)
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const f32x4 x = mine ? own[h][i][g] : pv[h][b][i * G + g];
-            if (k < n[h]) {
-              f32x4& d = h ? accL[i][g] : accF[i][g];
-              d = k == 0 ? x : d + x;
-            }
-          }
+          for (int g = 0; g < G; ++g) acc[i][g] = k == 0 ? ring[b][i * G + g] : acc[i][g] + ring[b][i * G + g];
+        if (k == 0) LQ_TS(8);
       }
     }
   }
@@ -415,7 +421,7 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
 
 template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
-  constexpr int T = tiles_per_wave<PAIR>();
+  constexpr int T = tiles_per_wave(WF, PAIR);
   constexpr int PF = pf_stages<T>(G);
   // G <= 2: a chunk's activation operands (all four steps) are read from LDS one chunk ahead, into registers,
   // through a ring of three LDS slots; larger G reads them within the chunk from a ring of two.
@@ -428,6 +434,23 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ int last_flag[2];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, t = lane >> 4;
+  unsigned long long ts[16] = {};
+  LQ_TS(0);
+  // One field of every 64-byte line of the arguments, read in one batch: later argument reads then hit the
+  // scalar cache instead of making dependent cold round trips (about a microsecond each) before the first
+  // weight load can issue.
+  asm volatile("" ::"s"(a.x), "s"(a.w[2]), "s"(a.svec[2]), "s"(a.resid[0]), "s"(a.tg0[4]));
+  LQ_TS(10);
+  auto flush_trace = [&](int pid) {
+#ifdef LQ_STREAM_TRACE
+    LQ_TS(6);
+    if (a.trace && threadIdx.x == 0)
+      for (int k = 0; k < 16; ++k) a.trace[pid * 16 + k] = ts[k];
+#else
+    (void)pid;
+    (void)ts;
+#endif
+  };
 
   if constexpr (WF == kFp4Coded) {
     for (int i = threadIdx.x; i < a.count * 64; i += kThreads) tabs[i >> 6][i & 63] = a.table[i >> 6][i & 63];
@@ -440,7 +463,10 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   if ((a.P & 7) == 0) p = (blockIdx.x & 7) * (a.P >> 3) + (blockIdx.x >> 3);
   const int u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
   const int n_it = u1 - u0;  // chunks this workgroup streams
-  if (n_it <= 0) return;
+  if (n_it <= 0) {
+    flush_trace(p);
+    return;
+  }
   const int tg_first = u0 / a.C, tg_last = (u1 - 1) / a.C;
   const int cfirst = u0 - tg_first * a.C;
 
@@ -464,6 +490,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   int ltg = tg_first, lc = cfirst, lleft = n_it;
   SegTiles<WF, T, PAIR> L;
   seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
+  LQ_TS(11);
   int ctg = tg_first, cc = cfirst;
   int cmi = L.mi, cwtile0 = L.wtile0;
 
@@ -498,23 +525,20 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
     for (int i = 0; i < G; ++i) *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
   };
 
-  // Accumulators are split by MFMA step parity; the first tile group's sums wait in accF for the end of the
-  // stream, a tile group wholly inside the range is finished where it ends.
-  f32x4 acc2[2][T][G], accF[T][G];
+  // The first tile group's sums wait in accF for the end of the stream; a tile group wholly inside the range
+  // is finished where it ends.
+  f32x4 acc2[T][G], accF[T][G];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int i = 0; i < T; ++i)
 #pragma unroll
-    for (int i = 0; i < T; ++i)
-#pragma unroll
-      for (int g = 0; g < G; ++g) acc2[h][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < G; ++g) acc2[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
   auto fold = [&](f32x4 (&out)[T][G]) {
 #pragma unroll
     for (int i = 0; i < T; ++i)
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        out[i][g] = acc2[0][i][g] + acc2[1][i][g];
-        acc2[0][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-        acc2[1][i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        out[i][g] = acc2[i][g];
+        acc2[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
   };
   auto after_chunk = [&](int it) {
@@ -525,8 +549,8 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
         f32x4 accM[T][G];
         fold(accM);
         EpiIn<G, T> eM;
-        epi_load<G, PAIR, OUTF32>(a, cmi, cwtile0, eM, r, t);
-        epilogue<G, PAIR, OUTF32>(a, cmi, cwtile0, accM, eM, r, t);
+        epi_load<G, PAIR, OUTF32, T>(a, cmi, cwtile0, eM, r, t);
+        epilogue<G, PAIR, OUTF32, T>(a, cmi, cwtile0, accM, eM, r, t);
         // Let these stores complete here: with stores of unknown completion order in flight, every later wait
         // on the ring would have to drain it (vmcnt(0)); after this wait the ring's waits stay partial.
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
@@ -549,12 +573,18 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   seg_tiles<WF, T, PAIR>(a, tg_first, wave, sF);
   seg_tiles<WF, T, PAIR>(a, tg_last, wave, sL);
   EpiIn<G, T> eF, eL;
-  epi_load<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, eF, r, t);
-  epi_load<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, eL, r, t);
+  epi_load<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, eF, r, t);
+  LQ_TS(12);
+  epi_load<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, eL, r, t);
+  LQ_TS(13);
 
   const int npad = (n_it + PF - 1) / PF * PF;
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) load_stage(j);
+  for (int j = 0; j < PF - 1; ++j) {
+    load_stage(j);
+    if (j == 0) LQ_TS(14);
+  }
+  LQ_TS(7);
   if constexpr (BPRE) {
     u32x4 bc[4][G], bn[4][G];
     put_x(0, 0);
@@ -576,6 +606,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
           tables(tab);
 #pragma unroll
           for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
+          if (it == 0) LQ_TS(1);
           after_chunk(it);
         }
 #pragma unroll
@@ -596,6 +627,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
           const uint8_t* tab[T];
           tables(tab);
           compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
+          if (it == 0) LQ_TS(1);
           after_chunk(it);
         }
       }
@@ -603,6 +635,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   }
   f32x4 accL[T][G];
   fold(accL);
+  LQ_TS(2);
 
   // Finish the first and the last tile group of the range: a whole one directly, a split one through the
   // partial exchange (every workgroup publishes, counts its arrival, and the last to arrive adds them).
@@ -613,15 +646,19 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   const bool splitL = !(lbeg == 0 && lend == a.C);
   if (!one) {
     if (splitF) publish_partial<G, T>(a, p, 0, accF, r);
-    else epilogue<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+    else epilogue<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, accF, eF, r, t);
   }
   if (splitL) publish_partial<G, T>(a, p, one ? 0 : 1, accL, r);
-  else epilogue<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, accL, eL, r, t);
-  if (!splitF && !splitL) return;
+  else epilogue<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, accL, eL, r, t);
+  if (!splitF && !splitL) {
+    flush_trace(p);
+    return;
+  }
   // Each thread waits for its own partial stores to complete before the barrier; only then does thread 0
   // count the workgroup's arrival.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  LQ_TS(3);
   const SplitInfo si[2] = {split_info(a, tg_first), split_info(a, tg_last)};
   // (selects rather than indexing si by thread: a thread-indexed local array would be placed in LDS)
   if (threadIdx.x < 2) {
@@ -638,10 +675,23 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   }
   __syncthreads();
   const bool doit[2] = {last_flag[0] != 0, last_flag[1] != 0};
-  if (!doit[0] && !doit[1]) return;
-  reduce_partials<G, T>(a, p, doit, si, accF, accL, r);
-  if (doit[0]) epilogue<G, PAIR, OUTF32>(a, sF.mi, sF.wtile0, accF, eF, r, t);
-  if (doit[1]) epilogue<G, PAIR, OUTF32>(a, sL.mi, sL.wtile0, accL, eL, r, t);
+  LQ_TS(4);
+  if (!doit[0] && !doit[1]) {
+    flush_trace(p);
+    return;
+  }
+  if (doit[0]) {
+    reduce_partials<G, T>(a, si[0], accF, r, ts);
+    LQ_TS(9);
+    epilogue<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+  }
+  if (doit[1]) {
+    reduce_partials<G, T>(a, si[1], accL, r, ts);
+    LQ_TS(9);
+    epilogue<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, accL, eL, r, t);
+  }
+  LQ_TS(5);
+  flush_trace(p);
 }
 
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
@@ -757,6 +807,10 @@ int launch_m(const StreamArgs& a, hipStream_t s) {
 
 // Validates, fills the launch arguments and launches. `fmt`: weight format; `f16`: activations are an
 // FP16 row copy (with xinv) rather than BF16; `pair`: mats = {gate, up} with the SiLU*mul epilogue.
+#ifdef LQ_STREAM_TRACE
+unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the next launches
+#endif
+
 int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, const void* x, const float* xinv, int M,
                   const Mat* mats, int n, int K, hipStream_t s) {
   const std::string nm(name);
@@ -791,11 +845,11 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     a.N[i] = m.N;
     a.ldy[i] = m.ldy;
     a.tg0[i] = tg;
-    if (!pair) tg += cdiv(m.N, kGroupRows);
+    if (!pair) tg += cdiv(m.N, group_rows(fmt, false));
   }
   if (pair) {
     if (n != 2 || mats[0].N != mats[1].N) return fail(LQ_ERR_SHAPE, nm + ": gate and up must have the same N");
-    tg = cdiv(mats[0].N, kGroupRows);
+    tg = cdiv(mats[0].N, group_rows(fmt, true));
   }
   a.tg0[n] = tg;
   a.TG = tg;
@@ -805,11 +859,14 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   a.U = static_cast<int>(units);
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  const size_t slot_floats = static_cast<size_t>(2) * cdiv(M, 16) * 4 * kThreads;
+  const size_t slot_floats = static_cast<size_t>(tiles_per_wave(fmt, pair)) * cdiv(M, 16) * 4 * kThreads;
   int rc = ws->reserve_stream(static_cast<size_t>(2) * a.P * slot_floats * sizeof(float), static_cast<size_t>(tg));
   if (rc) return rc;
   a.partials = ws->partials;
   a.counters = ws->counters;
+#ifdef LQ_STREAM_TRACE
+  a.trace = g_trace;
+#endif
   if (pair) return f16 ? launch_m<kFp8, true, true, false>(a, s) : launch_m<kFp8, false, true, false>(a, s);
   if (fmt == kFp8) {
     if (f16) return outf32 ? launch_m<kFp8, true, false, true>(a, s) : launch_m<kFp8, true, false, false>(a, s);
@@ -849,6 +906,14 @@ int half_rows(bool bf16in, const void* x, int M, int K, uint16_t* xh, float* xin
 using namespace lq;
 
 extern "C" {
+
+#ifdef LQ_STREAM_TRACE
+// Trace builds only: stream launches record per-workgroup phase stamps into `buf` ([P][8] u64, device).
+int lq_debug_stream_trace(unsigned long long* buf) {
+  g_trace = buf;
+  return LQ_OK;
+}
+#endif
 
 int lq_to_half_rows(const float* x, int M, int K, uint16_t* xh, float* xinv, void* stream) {
   return half_rows(false, x, M, K, xh, xinv, static_cast<hipStream_t>(stream));
