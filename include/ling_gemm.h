@@ -117,6 +117,17 @@ int lq_stream_fp8_pc_silu_mul(const uint16_t* x, int M, const uint8_t* w_gate, c
  * with the residual add fused (reference engine.cpp:1227-1233 linear_fp8_residual = stream_gemm + add_inplace). */
 int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n,
                               const uint16_t* resid, uint16_t* y, int N, int K, void* stream);
+/* The whole MLP step in one launch: h[M][I] = bf16(silu(sg . x G^T) * (su . x U^T)) (as stream_fp8_pc_silu_mul,
+ * K = H), then y[M][H] = bf16(sd . h D^T + resid) (as stream_fp8_pc_residual, K = I); y may be resid. Bit for bit
+ * the two calls' results. The launch keeps every workgroup resident (one per CU) and hands h from the first
+ * phase to the second inside the kernel: only one such launch may run on a device at a time. Replaces the
+ * reference's persistent FFN kernel (reference src/core/stream_gemm.cu:841-1072, ffn_step) for the FP8 rows path. */
+int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate, const uint8_t* w_up,
+                         const float* s_up, const uint8_t* w_down, const float* s_down, const uint16_t* resid,
+                         uint16_t* h, uint16_t* y, int I, int H, void* stream);
+/* Synchronous: *hit = 1 if a stream_fp8_pc_ffn launch on the current device ever gave up its in-kernel wait at
+ * the deadline (its results are then not valid), else 0. No counterpart in the reference (its wait traps). */
+int lq_stream_ffn_deadline_status(int* hit);
 /* y[M][N] = bf16(scale2 * x . W^T), W tiled NVFP4 (raw, or coded with its device table), x BF16: converts x
  * to the FP16 row copy in the workspace, then streams. Replaces linear_fp4 (engine.cpp:1173-1177). */
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,

@@ -96,6 +96,11 @@ inline void stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, c
                                    const uint16_t* resid, uint16_t* y, int N, int K, hipStream_t s) {
   lq_check(lq_stream_fp8_pc_residual(x, M, w, wscale_n, resid, y, N, K, s));
 }
+inline void stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate,
+                              const uint8_t* w_up, const float* s_up, const uint8_t* w_down, const float* s_down,
+                              const uint16_t* resid, uint16_t* h, uint16_t* y, int I, int H, hipStream_t s) {
+  lq_check(lq_stream_fp8_pc_ffn(x, M, w_gate, s_gate, w_up, s_up, w_down, s_down, resid, h, y, I, H, s));
+}
 inline void stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2,
                               uint16_t* y, int N, int K, hipStream_t s) {
   lq_check(lq_stream_nvfp4_bf16(x, M, w, table, scale2, y, N, K, s));

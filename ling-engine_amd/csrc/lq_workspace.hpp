@@ -1,6 +1,6 @@
 // Per-device workspace of the skinny GEMMs: split-K partial sums, per-tile-group arrival counters (kept
 // zero between launches: the last workgroup of a group resets its counter), and the FP16 activation copy
-// of the BF16-input NVFP4 entry point. Grow-only; allocated on first use or by lq_init().
+// of the BF16-input NVFP4 entry point, and the fused FFN launch's counters. Grow-only; allocated on first use or by lq_init().
 #pragma once
 
 #include <cstddef>
@@ -13,6 +13,7 @@ struct Workspace {
   size_t partial_bytes = 0;
   int* counters = nullptr;
   size_t counter_count = 0;
+  int* sync = nullptr;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
   uint16_t* xh = nullptr;
   float* xinv = nullptr;
   size_t half_elems = 0;

@@ -71,6 +71,12 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
       return fail(LQ_ERR_DEVICE, "workspace: counter allocation failed");
     counter_count = cap;
   }
+  if (!sync) {
+    if (hipMalloc(&sync, 16 * sizeof(int)) != hipSuccess || hipMemset(sync, 0, 16 * sizeof(int)) != hipSuccess) {
+      sync = nullptr;
+      return fail(LQ_ERR_DEVICE, "workspace: counter allocation failed");
+    }
+  }
   return LQ_OK;
 }
 

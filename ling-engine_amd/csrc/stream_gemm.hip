@@ -96,7 +96,7 @@ static_assert(sizeof(StreamArgs) <= 320 && offsetof(StreamArgs, x) / 64 == 0 &&
 // Phase stamps of a workgroup for builds with LQ_STREAM_TRACE: kept in registers, written once at exit.
 // 0 entry, 1 first chunk computed, 2 stream done, 3 partials published, 4 arrival counted, 5 reduced, 6 exit,
 // 7 prologue loads issued, 8 first partial added, 9 reduction loop done, 10 arguments read, 11 tiles set up,
-// 12 / 13 first / last epilogue inputs issued, 14 first ring stage issued.
+// 12 / 13 first / last epilogue inputs issued, 14 first ring stage issued, 15 activations ready.
 #ifdef LQ_STREAM_TRACE
 #define LQ_TS(i) (ts[i] = __builtin_amdgcn_s_memrealtime())
 #else
@@ -248,8 +248,9 @@ __device__ __forceinline__ void epi_load(const StreamArgs& a, int mi, int wtile0
   }
 }
 
-// Epilogue of one lane's outputs: acc[i][g][v] is row 16 * tile(i) + 4t + v, token 16g + r.
-template <int G, bool PAIR, bool OUTF32, int T>
+// Epilogue of one lane's outputs: acc[i][g][v] is row 16 * tile(i) + 4t + v, token 16g + r. COH: the stores
+// write through to memory (agent-coherent), for a consumer on another CU within the same launch.
+template <int G, bool PAIR, bool OUTF32, int T, bool COH = false>
 __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0, const f32x4 (&acc)[T][G],
                                          const EpiIn<G, T>& e, int r, int t) {
 #pragma unroll
@@ -269,7 +270,12 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
           o[v] = f32_to_bf16(silu(gs) * us);
         }
         uint16_t* dst = reinterpret_cast<uint16_t*>(a.y[0]) + static_cast<size_t>(tok) * a.ldy[0] + n;
-        *reinterpret_cast<u32x2*>(dst) = u32x2{o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16)};
+        const u32x2 pk{o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16)};
+        if constexpr (COH)
+          __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), __builtin_bit_cast(uint64_t, pk), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        else
+          *reinterpret_cast<u32x2*>(dst) = pk;
       }
     } else {
 #pragma unroll
@@ -360,49 +366,62 @@ __device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
   return s;
 }
 
-// The finishing step of a split tile group: the last workgroup to arrive adds every workgroup's partial in
+// The finishing step of split tile groups: the last workgroup to arrive adds every workgroup's partial in
 // workgroup order. Every workgroup (the finisher included) published its partial before arriving, so all of
-// them are read back from memory, D partials per batch: a batch's loads are all issued before its adds, so a
-// fan-in of up to D costs one memory round trip.
-template <int G, int T>
-__device__ __forceinline__ void reduce_partials(const StreamArgs& a, const SplitInfo& si, f32x4 (&acc)[T][G], int r,
+// them are read back from memory, D partials of each group per batch: a batch's loads (of both groups, when
+// this workgroup finishes its first and its last tile group) are all issued before its adds, so a fan-in of up
+// to D costs one memory round trip.
+template <int G, int T, int NG>
+__device__ __forceinline__ void reduce_partials(const StreamArgs& a, const SplitInfo* si, f32x4 (*acc[NG])[G], int r,
                                                 unsigned long long (&ts)[16]) {
   constexpr int NV = T * G;  // accumulator vectors per thread
-  constexpr int D = NV <= 4 ? 8 : NV <= 8 ? 4 : NV <= 10 ? 3 : NV <= 16 ? 2 : 1;
+  constexpr int D0 = NV <= 4 ? 8 : NV <= 8 ? 4 : NV <= 10 ? 3 : NV <= 16 ? 2 : 1;
+  constexpr int D = NG == 2 ? (D0 + 1) / 2 : D0;
   const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
-  const int n = si.pl - si.pf + 1;
+  int n[NG];
+  int nmax = 0;
+#pragma unroll
+  for (int h = 0; h < NG; ++h) {
+    n[h] = si[h].pl - si[h].pf + 1;
+    nmax = max(nmax, n[h]);
+  }
   // rows past M read nothing (an out-of-range offset returns zeros): they only reach outputs never stored
   unsigned rowmask[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) rowmask[g] = 16 * g + r < a.M ? 0u : 0x80000000u;
-  f32x4 ring[D][NV];
+  f32x4 ring[NG][D][NV];
   // Only positions that exist are loaded (out-of-range buffer loads are not free: a burst of them delays the
   // wanted ones).
-  auto issue = [&](int k, int b) {
-    if (k >= n) return;
-    const int off = slot_off<G, T>(si.pf + k, (k > 0 || si.pf_first) ? 0 : 1);
+  auto issue = [&](int h, int k, int b) {
+    if (k >= n[h]) return;
+    const int off = slot_off<G, T>(si[h].pf + k, (k > 0 || si[h].pf_first) ? 0 : 1);
 #pragma unroll
     for (int i = 0; i < T; ++i)
 #pragma unroll
       for (int g = 0; g < G; ++g)
-        ring[b][i * G + g] = __builtin_bit_cast(
+        ring[h][b][i * G + g] = __builtin_bit_cast(
             f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                        prs, static_cast<int>((off + (i * G + g) * 16 * kThreads) | rowmask[g]), 0, kSc1));
   };
-  for (int q0 = 0; q0 < n; q0 += D) {
+  for (int q0 = 0; q0 < nmax; q0 += D) {
 #pragma unroll
-    for (int b = 0; b < D; ++b) issue(q0 + b, b);
+    for (int h = 0; h < NG; ++h)
 #pragma unroll
-    for (int b = 0; b < D; ++b) {
-      const int k = q0 + b;
-      if (k < n) {
+      for (int b = 0; b < D; ++b) issue(h, q0 + b, b);
 #pragma unroll
-        for (int i = 0; i < T; ++i)
+    for (int h = 0; h < NG; ++h)
 #pragma unroll
-          for (int g = 0; g < G; ++g) acc[i][g] = k == 0 ? ring[b][i * G + g] : acc[i][g] + ring[b][i * G + g];
-        if (k == 0) LQ_TS(8);
+      for (int b = 0; b < D; ++b) {
+        const int k = q0 + b;
+        if (k < n[h]) {
+#pragma unroll
+          for (int i = 0; i < T; ++i)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+              acc[h][i][g] = k == 0 ? ring[h][b][i * G + g] : acc[h][i][g] + ring[h][b][i * G + g];
+          if (k == 0) LQ_TS(8);
+        }
       }
-    }
   }
 }
 
@@ -419,19 +438,52 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
         __builtin_amdgcn_raw_buffer_store_b128(acc[i][g], prs, off + (i * G + g) * 16 * kThreads, 0, kSc1);
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
-__global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
+// G <= 2: a chunk's activation operands (all four steps) are read from LDS one chunk ahead, into registers,
+// through a ring of three LDS slots; larger G reads them within the chunk from a ring of two.
+template <int G>
+struct Smem {
+  static constexpr bool BPRE = G <= 2;
+  static constexpr int NSLOT = BPRE ? 3 : 2;
+  static constexpr int XS_BYTES = 16 * G * 256;  // one chunk of activations, 16G rows
+  uint8_t xs[NSLOT][XS_BYTES];
+  uint8_t tabs[kMaxMats][64];
+  int last_flag[2];
+};
+
+// Body modes: kYCoh = the pair epilogue's stores write through (a later phase of the same launch reads them);
+// kXCoh = activations are read agent-coherently and only after `ready()` returns (the weight ring's first
+// stages are issued before the wait).
+constexpr int kYCoh = 1, kXCoh = 2;
+
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// Logical workgroup id: blockIdx.x % 8 is the XCD the hardware places it on; consecutive logical ids share an
+// XCD, so a tile group's partials are exchanged within one L2.
+__device__ __forceinline__ int logical_wg(int P) {
+  int p = blockIdx.x;
+  if ((P & 7) == 0) p = (blockIdx.x & 7) * (P >> 3) + (blockIdx.x >> 3);
+  return p;
+}
+
+template <int G, int WF, bool F16, bool PAIR, bool OUTF32, int MODE, class Ready>
+__device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>& sm, Ready&& ready) {
   constexpr int T = tiles_per_wave(WF, PAIR);
   constexpr int PF = pf_stages<T>(G);
-  // G <= 2: a chunk's activation operands (all four steps) are read from LDS one chunk ahead, into registers,
-  // through a ring of three LDS slots; larger G reads them within the chunk from a ring of two.
-  constexpr bool BPRE = G <= 2;
-  constexpr int NSLOT = BPRE ? 3 : 2;
-  constexpr int XS_BYTES = 16 * G * 256;  // one chunk of activations, 16G rows
+  constexpr bool BPRE = Smem<G>::BPRE;
+  constexpr int NSLOT = Smem<G>::NSLOT;
+#ifdef LQ_EXP_PLAIN
+  constexpr bool YCOH = false, XCOH = (MODE & kXCoh) != 0;
+  constexpr int XPOL = 0;
+#else
+  constexpr bool YCOH = (MODE & kYCoh) != 0, XCOH = (MODE & kXCoh) != 0;
+  constexpr int XPOL = XCOH ? kSc1 : 0;
+#endif
   static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
-  __shared__ __attribute__((aligned(16))) uint8_t xs[NSLOT][XS_BYTES];
-  __shared__ uint8_t tabs[kMaxMats][64];
-  __shared__ int last_flag[2];
+  auto& xs = sm.xs;
+  auto& tabs = sm.tabs;
+  auto& last_flag = sm.last_flag;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, t = lane >> 4;
   unsigned long long ts[16] = {};
@@ -457,10 +509,6 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
     __syncthreads();
   }
 
-  // Logical workgroup id: blockIdx.x % 8 is the XCD the hardware places it on; consecutive logical ids
-  // share an XCD, so a tile group's partials are exchanged within one L2.
-  int p = blockIdx.x;
-  if ((a.P & 7) == 0) p = (blockIdx.x & 7) * (a.P >> 3) + (blockIdx.x >> 3);
   const int u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
   const int n_it = u1 - u0;  // chunks this workgroup streams
   if (n_it <= 0) {
@@ -499,18 +547,13 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   // Every ring load is issued unconditionally (the wait counts then hold on every path); a load past the
   // stream's end is turned into an out-of-range buffer load (offset >= num_records), which returns zeros and
   // touches no memory.
-  auto load_stage = [&](int j) {
-    const unsigned oob = lleft > 0 ? 0u : 0x80000000u;
-    // scheduling barriers keep the issue order (activations, then weights, chunk after chunk) that the
-    // in-order wait counts rely on
-    __builtin_amdgcn_sched_barrier(0);
+  auto load_x = [&](int j, int lcj, unsigned oob) {
 #pragma unroll
     for (int i = 0; i < G; ++i)
       xr[j][i] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i] | oob), lc * 256, 0));
-    __builtin_amdgcn_sched_barrier(0);
-    load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | oob), slot, oob);
-    __builtin_amdgcn_sched_barrier(0);
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i] | oob), lcj * 256, XPOL));
+  };
+  auto advance = [&]() {
     if (lleft > 0) {
       --lleft;
       if (++lc == a.C) {
@@ -519,6 +562,17 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
         if (lleft > 0) seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
       }
     }
+  };
+  auto load_stage = [&](int j) {
+    const unsigned oob = lleft > 0 ? 0u : 0x80000000u;
+    // scheduling barriers keep the issue order (activations, then weights, chunk after chunk) that the
+    // in-order wait counts rely on
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(j, lc, oob);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | oob), slot, oob);
+    __builtin_amdgcn_sched_barrier(0);
+    advance();
   };
   auto put_x = [&](int j, int sl) {
 #pragma unroll
@@ -550,7 +604,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
         fold(accM);
         EpiIn<G, T> eM;
         epi_load<G, PAIR, OUTF32, T>(a, cmi, cwtile0, eM, r, t);
-        epilogue<G, PAIR, OUTF32, T>(a, cmi, cwtile0, accM, eM, r, t);
+        epilogue<G, PAIR, OUTF32, T, YCOH>(a, cmi, cwtile0, accM, eM, r, t);
         // Let these stores complete here: with stores of unknown completion order in flight, every later wait
         // on the ring would have to drain it (vmcnt(0)); after this wait the ring's waits stay partial.
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt and lgkmcnt unconstrained (gfx9 encoding)
@@ -579,10 +633,27 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   LQ_TS(13);
 
   const int npad = (n_it + PF - 1) / PF * PF;
+  if constexpr (XCOH) {
+    // weights of the first stages first, then the wait for the activations, then their loads
+    int lcs[PF - 1];
+    unsigned oobs[PF - 1];
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j) {
-    load_stage(j);
-    if (j == 0) LQ_TS(14);
+    for (int j = 0; j < PF - 1; ++j) {
+      oobs[j] = lleft > 0 ? 0u : 0x80000000u;
+      lcs[j] = lc;
+      load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | oobs[j]), slot, oobs[j]);
+      advance();
+    }
+    ready();
+    LQ_TS(15);
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) load_x(j, lcs[j], oobs[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) {
+      load_stage(j);
+      if (j == 0) LQ_TS(14);
+    }
   }
   LQ_TS(7);
   if constexpr (BPRE) {
@@ -646,10 +717,10 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   const bool splitL = !(lbeg == 0 && lend == a.C);
   if (!one) {
     if (splitF) publish_partial<G, T>(a, p, 0, accF, r);
-    else epilogue<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+    else epilogue<G, PAIR, OUTF32, T, YCOH>(a, sF.mi, sF.wtile0, accF, eF, r, t);
   }
   if (splitL) publish_partial<G, T>(a, p, one ? 0 : 1, accL, r);
-  else epilogue<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, accL, eL, r, t);
+  else epilogue<G, PAIR, OUTF32, T, YCOH>(a, sL.mi, sL.wtile0, accL, eL, r, t);
   if (!splitF && !splitL) {
     flush_trace(p);
     return;
@@ -680,18 +751,72 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
     flush_trace(p);
     return;
   }
-  if (doit[0]) {
-    reduce_partials<G, T>(a, si[0], accF, r, ts);
-    LQ_TS(9);
-    epilogue<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+  // Both groups' reductions share their round trips when their rings fit in registers (T x G <= 8).
+  if (T * G <= 8 && doit[0] && doit[1]) {
+    f32x4 (*accs[2])[G] = {accF, accL};
+    reduce_partials<G, T, (T * G <= 8 ? 2 : 1)>(a, si, accs, r, ts);
+  } else {
+    if (doit[0]) {
+      f32x4 (*accs[1])[G] = {accF};
+      reduce_partials<G, T, 1>(a, si, accs, r, ts);
+    }
+    if (doit[1]) {
+      f32x4 (*accs[1])[G] = {accL};
+      reduce_partials<G, T, 1>(a, si + 1, accs, r, ts);
+    }
   }
-  if (doit[1]) {
-    reduce_partials<G, T>(a, si[1], accL, r, ts);
-    LQ_TS(9);
-    epilogue<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, accL, eL, r, t);
-  }
+  LQ_TS(9);
+  if (doit[0]) epilogue<G, PAIR, OUTF32, T, YCOH>(a, sF.mi, sF.wtile0, accF, eF, r, t);
+  if (doit[1]) epilogue<G, PAIR, OUTF32, T, YCOH>(a, sL.mi, sL.wtile0, accL, eL, r, t);
   LQ_TS(5);
   flush_trace(p);
+}
+
+template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
+__global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
+  __shared__ __attribute__((aligned(16))) Smem<G> sm;
+  stream_body<G, WF, F16, PAIR, OUTF32, 0>(a, logical_wg(a.P), sm, NoWait{});
+}
+
+// The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
+// with SiLU(gate) * up into h (a), phase B = down (+ residual) from h (b). Both phases use the same P and the
+// same split as two separate launches, so every output is bit for bit theirs. Each workgroup ends phase A
+// with its h stores complete and counts itself on sync[0]; phase B issues its first weight stages, then waits
+// until all P have arrived (a workgroup that finished phase A early spends the wait with weights in flight),
+// then reads h agent-coherently. Requires all P workgroups to be resident at once (P <= #CUs, one launch of
+// this kernel per device at a time); a wait past its deadline records sync[2] = 1 and goes on, so the
+// kernel always exits. The last workgroup out resets the counters (no memset node in a captured graph).
+constexpr unsigned long long kFfnDeadlineTicks = 10'000'000ull;  // s_memrealtime at 100 MHz: 100 ms
+
+template <int G>
+__global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const StreamArgs b, int* sync) {
+  __shared__ __attribute__((aligned(16))) Smem<G> sm;
+  const int p = logical_wg(a.P);
+  stream_body<G, kFp8, false, true, false, kYCoh>(a, p, sm, NoWait{});
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int P = a.P;
+  auto ready = [&]() {
+    if (threadIdx.x == 0) {
+      const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+      while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < P) {
+        __builtin_amdgcn_s_sleep(2);
+        if (__builtin_amdgcn_s_memrealtime() - t0 > kFfnDeadlineTicks) {
+          __hip_atomic_store(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+      }
+    }
+    __syncthreads();
+  };
+  stream_body<G, kFp8, false, false, false, kXCoh>(b, p, sm, ready);
+  __syncthreads();
+  if (threadIdx.x == 0 &&
+      __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1) {
+    __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
@@ -811,15 +936,21 @@ int launch_m(const StreamArgs& a, hipStream_t s) {
 unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the next launches
 #endif
 
-int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, const void* x, const float* xinv, int M,
-                  const Mat* mats, int n, int K, hipStream_t s) {
+// FP32 floats of one partial slot (one workgroup's T x G accumulator vectors for 256 threads).
+size_t slot_floats(int fmt, bool pair, int M) {
+  return static_cast<size_t>(tiles_per_wave(fmt, pair)) * cdiv(M, 16) * 4 * kThreads;
+}
+
+// Validates and fills the launch arguments except the workspace pointers.
+int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, const void* x, const float* xinv, int M,
+                const Mat* mats, int n, int K, StreamArgs& a) {
   const std::string nm(name);
   if (K <= 0 || K % kChunk != 0) return fail(LQ_ERR_SHAPE, nm + ": K must be a multiple of 128");
   if (M < 1 || M > LQ_MAX_STREAM_ROWS) return fail(LQ_ERR_SHAPE, nm + ": M must be in [1, 80]");
   if (n < 1 || n > kMaxMats) return fail(LQ_ERR_SHAPE, nm + ": 1 to 4 matrices per launch");
   if (!x) return fail(LQ_ERR_ARG, nm + ": null activations");
   if (f16 && !xinv) return fail(LQ_ERR_ARG, nm + ": null xinv");
-  StreamArgs a{};
+  a = StreamArgs{};
   a.x = x;
   a.xinv = xinv;
   a.M = M;
@@ -857,10 +988,19 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   a.P = choose_wgs(units);
   if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrices too large for one launch");
   a.U = static_cast<int>(units);
+  if (!pair && fmt != kFp8 && !f16) return fail(LQ_ERR_ARG, nm + ": NVFP4 streams FP16 activations");
+  return LQ_OK;
+}
+
+int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, const void* x, const float* xinv, int M,
+                  const Mat* mats, int n, int K, hipStream_t s) {
+  StreamArgs a;
+  int rc = stream_args(name, fmt, f16, pair, outf32, x, xinv, M, mats, n, K, a);
+  if (rc) return rc;
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  const size_t slot_floats = static_cast<size_t>(tiles_per_wave(fmt, pair)) * cdiv(M, 16) * 4 * kThreads;
-  int rc = ws->reserve_stream(static_cast<size_t>(2) * a.P * slot_floats * sizeof(float), static_cast<size_t>(tg));
+  rc = ws->reserve_stream(2 * static_cast<size_t>(a.P) * slot_floats(fmt, pair, M) * sizeof(float),
+                          static_cast<size_t>(a.TG));
   if (rc) return rc;
   a.partials = ws->partials;
   a.counters = ws->counters;
@@ -872,9 +1012,45 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     if (f16) return outf32 ? launch_m<kFp8, true, false, true>(a, s) : launch_m<kFp8, true, false, false>(a, s);
     return outf32 ? launch_m<kFp8, false, false, true>(a, s) : launch_m<kFp8, false, false, false>(a, s);
   }
-  if (!f16) return fail(LQ_ERR_ARG, nm + ": NVFP4 streams FP16 activations");
   if (fmt == kFp4) return outf32 ? launch_m<kFp4, true, false, true>(a, s) : launch_m<kFp4, true, false, false>(a, s);
   return outf32 ? launch_m<kFp4Coded, true, false, true>(a, s) : launch_m<kFp4Coded, true, false, false>(a, s);
+}
+
+// The FFN step (gate|up + SiLU*mul into h, down + residual into y) as one launch when both phases get the same
+// number of workgroups, else as the two launches it equals bit for bit.
+int ffn_launch(const char* name, const uint16_t* x, int M, const Mat (&gu)[2], const Mat& dn, const uint16_t* h,
+               hipStream_t s) {
+  StreamArgs a, b;
+  int rc = stream_args(name, kFp8, false, true, false, x, nullptr, M, gu, 2, dn.N, a);
+  if (rc) return rc;
+  rc = stream_args(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, b);
+  if (rc) return rc;
+  if (a.P != b.P) {
+    rc = stream_launch(name, kFp8, false, true, false, x, nullptr, M, gu, 2, dn.N, s);
+    return rc ? rc : stream_launch(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, s);
+  }
+  Workspace* ws = workspace_for_current_device();
+  if (!ws) return LQ_ERR_DEVICE;
+  const size_t fa = 2 * static_cast<size_t>(a.P) * slot_floats(kFp8, true, M);
+  const size_t fb = 2 * static_cast<size_t>(b.P) * slot_floats(kFp8, false, M);
+  rc = ws->reserve_stream((fa + fb) * sizeof(float), static_cast<size_t>(a.TG) + b.TG);
+  if (rc) return rc;
+  a.partials = ws->partials;
+  a.counters = ws->counters;
+  b.partials = ws->partials + fa;
+  b.counters = ws->counters + a.TG;
+#ifdef LQ_STREAM_TRACE
+  a.trace = g_trace;
+  b.trace = g_trace ? g_trace + 16 * static_cast<size_t>(a.P) : nullptr;
+#endif
+  switch (cdiv(M, 16)) {
+    case 1: hipLaunchKernelGGL(ffn_kernel<1>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+    case 2: hipLaunchKernelGGL(ffn_kernel<2>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+    case 3: hipLaunchKernelGGL(ffn_kernel<3>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+    case 4: hipLaunchKernelGGL(ffn_kernel<4>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+    default: hipLaunchKernelGGL(ffn_kernel<5>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+  }
+  return check_launch(name);
 }
 
 // Shape checks first (the reference throws these before looking at pointers).
@@ -991,6 +1167,28 @@ int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const 
   const Mat m{w, nullptr, wscale_n, 0.f, y, resid, N, N};
   return stream_launch("stream_fp8_pc_residual", kFp8, false, false, false, x, nullptr, M, &m, 1, K,
                        static_cast<hipStream_t>(stream));
+}
+
+int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate, const uint8_t* w_up,
+                         const float* s_up, const uint8_t* w_down, const float* s_down, const uint16_t* resid,
+                         uint16_t* h, uint16_t* y, int I, int H, void* stream) {
+  if (int rc = check_rows("stream_fp8_pc_ffn", M, I, H)) return rc;
+  if (int rc = check_rows("stream_fp8_pc_ffn", M, H, I)) return rc;
+  if (!s_gate || !s_up || !s_down || !resid || !h) return fail(LQ_ERR_ARG, "stream_fp8_pc_ffn: null scales, residual or h");
+  const Mat gu[2] = {{w_gate, nullptr, s_gate, 0.f, h, nullptr, I, I}, {w_up, nullptr, s_up, 0.f, h, nullptr, I, I}};
+  const Mat dn{w_down, nullptr, s_down, 0.f, y, resid, H, H};
+  return ffn_launch("stream_fp8_pc_ffn", x, M, gu, dn, h, static_cast<hipStream_t>(stream));
+}
+
+int lq_stream_ffn_deadline_status(int* hit) {
+  if (!hit) return fail(LQ_ERR_ARG, "stream_ffn_deadline_status: null pointer");
+  Workspace* ws = workspace_for_current_device();
+  if (!ws) return LQ_ERR_DEVICE;
+  *hit = 0;
+  if (!ws->sync) return LQ_OK;
+  if (hipMemcpy(hit, ws->sync + 2, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: copy failed");
+  return LQ_OK;
 }
 
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,

@@ -40,6 +40,8 @@ SIGNATURES = {
     "lq_stream_fp8_pc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_residual": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_fp8_pc_ffn": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_ffn_deadline_status": (_I, [_P]),
     "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_quant_act_fp8_g128": (_I, [_P, _I, _I, _P, _P, _P]),
     "lq_prefill_fp8_block": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
@@ -255,6 +257,23 @@ def stream_fp8_pc_residual(x, w, wscale_n, resid, N: int, y=None):
     _check(lib.lq_stream_fp8_pc_residual(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(wscale_n),
                                          _ptr(_dev(resid, torch.bfloat16)), _ptr(y), N, K, _stream()))
     return y
+
+
+def stream_fp8_pc_ffn(x, w_gate, s_gate, w_up, s_up, w_down, s_down, resid, I: int, h=None, y=None):
+    """One launch: h = silu(gate) * up (BF16 [M][I]), y = down(h) + resid (BF16 [M][H]); returns (h, y)."""
+    M, H = x.shape
+    h = torch.empty((M, I), dtype=torch.bfloat16, device=x.device) if h is None else h
+    y = torch.empty((M, H), dtype=torch.bfloat16, device=x.device) if y is None else y
+    _check(lib.lq_stream_fp8_pc_ffn(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w_gate), _ptr(s_gate), _ptr(w_up),
+                                    _ptr(s_up), _ptr(w_down), _ptr(s_down), _ptr(_dev(resid, torch.bfloat16)),
+                                    _ptr(_dev(h, torch.bfloat16)), _ptr(_dev(y, torch.bfloat16)), I, H, _stream()))
+    return h, y
+
+
+def stream_ffn_deadline_status() -> int:
+    hit = C.c_int(0)
+    _check(lib.lq_stream_ffn_deadline_status(C.byref(hit)))
+    return hit.value
 
 
 def stream_nvfp4_bf16(x, w, table, scale2: float, N: int, y=None):

@@ -141,6 +141,58 @@ def test_stream_fp8_pc_residual_in_place(L):
     assert np.array_equal(bf16_host(rd), out)
 
 
+def _ffn_case(L, I, H, seed, Ms):
+    qg, sg = fp8_weights(seed, I, H)
+    qu, su = fp8_weights(seed + 1, I, H)
+    qd, sd = fp8_weights(seed + 2, H, I)
+    tg, tu, td = L.retile_fp8(to_dev(qg)), L.retile_fp8(to_dev(qu)), L.retile_fp8(to_dev(qd))
+    sg_d, su_d, sd_d = to_dev(sg), to_dev(su), to_dev(sd)
+    x = O.normal_bf16(seed + 3, 1.0, (max(Ms), H))
+    r = O.normal_bf16(seed + 4, 1.0, (max(Ms), H))
+    out = {}
+    for M in Ms:
+        xd, rd = bf16_dev(x[:M]), bf16_dev(r[:M])
+        h_sep = L.stream_fp8_pc_silu_mul(xd, tg, sg_d, tu, su_d, I)
+        y_sep = L.stream_fp8_pc_residual(h_sep, td, sd_d, rd, H)
+        for rep in range(3):  # repeated launches: the in-kernel counters reset themselves
+            h, y = L.stream_fp8_pc_ffn(xd, tg, sg_d, tu, su_d, td, sd_d, rd, I)
+            assert np.array_equal(bf16_host(h), bf16_host(h_sep)), f"ffn h M={M} launch {rep}"
+            assert np.array_equal(bf16_host(y), bf16_host(y_sep)), f"ffn y M={M} launch {rep}"
+        out[M] = (bf16_host(h), bf16_host(y))
+    assert L.stream_ffn_deadline_status() == 0
+    return (qg, sg, qu, su, qd, sd, x, r), out
+
+
+def test_stream_fp8_pc_ffn_one_launch(L):
+    """The one-launch FFN equals gate|up + SiLU*mul followed by down + residual bit for bit, and the oracle."""
+    I, H = 4096, 2048
+    (qg, sg, qu, su, qd, sd, x, r), out = _ffn_case(L, I, H, 40, [1, 17, 68])
+    M = 17
+    xf = O.bf16_to_f32(x[:M])
+    href = O.epi_silu_mul_bf16(O.gemm_f32(xf, O.dequant_fp8_pc(qg, sg)), O.gemm_f32(xf, O.dequant_fp8_pc(qu, su)))
+    yref = O.epi_residual_bf16(O.gemm_f32(O.bf16_to_f32(out[M][0]), O.dequant_fp8_pc(qd, sd)), r[:M])
+    assert_close_bf16(out[M][0], href, "ffn h")
+    assert_close_bf16(out[M][1], yref, "ffn y")
+
+
+def test_stream_fp8_pc_ffn_in_place_full_size(L):
+    """Config 2's shapes (I = 17408, H = 5120, M = 17) with the residual updated in place."""
+    I, H, M = 17408, 5120, 17
+    x = O.normal_bf16(99, 1.0, (M, H))
+    r = O.normal_bf16(98, 1.0, (M, H))
+    qg, sg = fp8_weights(60, I, H)
+    qu, su = fp8_weights(61, I, H)
+    qd, sd = fp8_weights(62, H, I)
+    tg, tu, td = L.retile_fp8(to_dev(qg)), L.retile_fp8(to_dev(qu)), L.retile_fp8(to_dev(qd))
+    xd, rd = bf16_dev(x), bf16_dev(r)
+    h_sep = L.stream_fp8_pc_silu_mul(xd, tg, to_dev(sg), tu, to_dev(su), I)
+    y_sep = bf16_host(L.stream_fp8_pc_residual(h_sep, td, to_dev(sd), rd, H))
+    h, y = L.stream_fp8_pc_ffn(xd, tg, to_dev(sg), tu, to_dev(su), td, to_dev(sd), rd, I, y=rd)
+    assert np.array_equal(bf16_host(h), bf16_host(h_sep))
+    assert np.array_equal(bf16_host(rd), y_sep)
+    assert L.stream_ffn_deadline_status() == 0
+
+
 # ---------------------------------------------------------------- reference-compatible FP16 path
 def reference_rows(x: np.ndarray, wdeq: np.ndarray) -> np.ndarray:
     return (x.astype(np.float64) @ wdeq.astype(np.float64).T)
