@@ -128,8 +128,9 @@ int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const 
 /* Synchronous: *hit = 1 if a stream_fp8_pc_ffn launch on the current device ever gave up its in-kernel wait at
  * the deadline (its results are then not valid), else 0. No counterpart in the reference (its wait traps). */
 int lq_stream_ffn_deadline_status(int* hit);
-/* y[M][N] = bf16(scale2 * x . W^T), W tiled NVFP4 (raw, or coded with its device table), x BF16: converts x
- * to the FP16 row copy in the workspace, then streams. Replaces linear_fp4 (engine.cpp:1173-1177). */
+/* y[M][N] = bf16(scale2 * x . W^T), W tiled NVFP4 (raw, or coded with its device table), x BF16. The kernel
+ * turns each 128-value chunk of a row of x into FP16 under a power-of-two scale from that chunk's largest
+ * magnitude and multiplies the chunk's sums back in FP32. Replaces linear_fp4 (engine.cpp:1173-1177). */
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
                          int N, int K, void* stream);
 

@@ -1,6 +1,6 @@
 // Per-device workspace of the skinny GEMMs: split-K partial sums, per-tile-group arrival counters (kept
-// zero between launches: the last workgroup of a group resets its counter), and the FP16 activation copy
-// of the BF16-input NVFP4 entry point, and the fused FFN launch's counters. Grow-only; allocated on first use or by lq_init().
+// zero between launches: the last workgroup of a group resets its counter) and the one-launch FFN's counters.
+// Grow-only; allocated on first use or by lq_init().
 #pragma once
 
 #include <cstddef>
@@ -14,12 +14,8 @@ struct Workspace {
   int* counters = nullptr;
   size_t counter_count = 0;
   int* sync = nullptr;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
-  uint16_t* xh = nullptr;
-  float* xinv = nullptr;
-  size_t half_elems = 0;
   // Ensure capacity; returns LQ_OK or LQ_ERR_DEVICE (message set).
   int reserve_stream(size_t partial_bytes_needed, size_t counters_needed);
-  int reserve_half(size_t elems);
 };
 
 // The calling thread's current device's workspace (created on first call), or null (error set).

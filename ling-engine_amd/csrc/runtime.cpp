@@ -80,22 +80,6 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
   return LQ_OK;
 }
 
-int Workspace::reserve_half(size_t elems) {
-  std::lock_guard<std::mutex> lock(g_mutex);
-  if (elems > half_elems) {
-    const size_t cap = std::max(elems, size_t(80) * 32768);
-    if (xh) (void)hipFree(xh);
-    if (xinv) (void)hipFree(xinv);
-    xh = nullptr;
-    xinv = nullptr;
-    half_elems = 0;
-    if (hipMalloc(&xh, cap * sizeof(uint16_t)) != hipSuccess || hipMalloc(&xinv, 128 * sizeof(float)) != hipSuccess)
-      return fail(LQ_ERR_DEVICE, "workspace: FP16 activation buffer allocation failed");
-    half_elems = cap;
-  }
-  return LQ_OK;
-}
-
 }  // namespace lq
 
 extern "C" {
@@ -108,8 +92,6 @@ int lq_init(void) {
   lq::Workspace* ws = lq::workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
   int rc = ws->reserve_stream(size_t(64) << 20, size_t(1) << 16);
-  if (rc) return rc;
-  rc = ws->reserve_half(size_t(80) * 32768);
   if (rc) return rc;
   return hipDeviceSynchronize() == hipSuccess ? LQ_OK : lq::fail(LQ_ERR_DEVICE, "lq_init: device synchronize failed");
 }

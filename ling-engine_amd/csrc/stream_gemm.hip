@@ -446,14 +446,44 @@ struct Smem {
   static constexpr int NSLOT = BPRE ? 3 : 2;
   static constexpr int XS_BYTES = 16 * G * 256;  // one chunk of activations, 16G rows
   uint8_t xs[NSLOT][XS_BYTES];
+  float xsc[NSLOT][16 * G];  // kCvt: 2^(e - 15) of each row's chunk in the slot
   uint8_t tabs[kMaxMats][64];
   int last_flag[2];
 };
 
 // Body modes: kYCoh = the pair epilogue's stores write through (a later phase of the same launch reads them);
 // kXCoh = activations are read agent-coherently and only after `ready()` returns (the weight ring's first
-// stages are issued before the wait).
-constexpr int kYCoh = 1, kXCoh = 2;
+// stages are issued before the wait); kCvt = BF16 activations become FP16 as each chunk is staged, with a
+// power-of-two scale per row and chunk (from the chunk's largest magnitude, as to_half_rows does per row) that
+// each chunk's MFMA sums are multiplied back by, in FP32, before they join the running sums.
+constexpr int kYCoh = 1, kXCoh = 2, kCvt = 4;
+
+// kCvt staging of one thread's 8 activations (a 16-byte unit of row `row`; the row's 16 units of the chunk are
+// in 16 consecutive lanes): returns them as FP16 scaled by 2^(15 - e), e = exponent of the chunk's largest
+// magnitude in the row (0 when that is zero or not finite), and stores 2^(e - 15) for the row.
+__device__ __forceinline__ u32x4 stage_cvt(const u32x4& v, float* xsc_row, bool writer) {
+  float f[8];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = __uint_as_float(w[k] << 16);
+    f[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(f[k]));
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+  int e = 0;
+  if (m > 0.f && isfinite(m)) frexpf(m, &e);
+  const float sc = ldexpf(1.f, 15 - e);
+  if (writer) *xsc_row = ldexpf(1.f, e - 15);
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    o[k] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f[2 * k] * sc, f[2 * k + 1] * sc));
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
 
 struct NoWait {
   __device__ void operator()() const {}
@@ -480,6 +510,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   constexpr bool YCOH = (MODE & kYCoh) != 0, XCOH = (MODE & kXCoh) != 0;
   constexpr int XPOL = XCOH ? kSc1 : 0;
 #endif
+  constexpr bool CVT = (MODE & kCvt) != 0;
+  static_assert(!CVT || F16, "converted activations feed the FP16 MFMA");
   static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
   auto& xs = sm.xs;
   auto& tabs = sm.tabs;
@@ -576,7 +608,26 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   };
   auto put_x = [&](int j, int sl) {
 #pragma unroll
-    for (int i = 0; i < G; ++i) *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
+    for (int i = 0; i < G; ++i) {
+      if constexpr (CVT) {
+        const int row = (i * kThreads + static_cast<int>(threadIdx.x)) >> 4;
+        *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = stage_cvt(xr[j][i], &sm.xsc[sl][row], (threadIdx.x & 15) == 0);
+      } else {
+        *reinterpret_cast<u32x4*>(xs[sl] + xdst[i]) = xr[j][i];
+      }
+    }
+  };
+  // kCvt: a chunk's MFMA sums (accc) join the running sums (acc2) times the row's chunk scale.
+  f32x4 accc[T][G];
+  auto clear_c = [&]() {
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g) accc[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  auto chunk_scales = [&](float (&scs)[G], int sl) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) scs[g] = sm.xsc[sl][16 * g + r];
   };
 
   // The first tile group's sums wait in accF for the end of the stream; a tile group wholly inside the range
@@ -586,6 +637,14 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   for (int i = 0; i < T; ++i)
 #pragma unroll
     for (int g = 0; g < G; ++g) acc2[i][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto fold_c = [&](const float (&scs)[G]) {
+#pragma unroll
+    for (int i = 0; i < T; ++i)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc2[i][g][v] = __builtin_fmaf(accc[i][g][v], scs[g], acc2[i][g][v]);
+  };
   auto fold = [&](f32x4 (&out)[T][G]) {
 #pragma unroll
     for (int i = 0; i < T; ++i)
@@ -658,10 +717,12 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   LQ_TS(7);
   if constexpr (BPRE) {
     u32x4 bc[4][G], bn[4][G];
+    float scc[G], scn[G];
     put_x(0, 0);
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < 4; ++s) read_b<G>(bc[s], xs[0], s, r, t);
+    if constexpr (CVT) chunk_scales(scc, 0);
     for (int base = 0; base < npad; base += PF) {
 #pragma unroll
       for (int j = 0; j < PF; ++j) {
@@ -672,11 +733,19 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
         load_stage((j + PF - 1) % PF);
 #pragma unroll
         for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
+        if constexpr (CVT) chunk_scales(scn, sl);
         if (it < n_it) {
           const uint8_t* tab[T];
           tables(tab);
+          if constexpr (CVT) {
+            clear_c();
 #pragma unroll
-          for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
+            for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], accc, tab);
+            fold_c(scc);
+          } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
+          }
           if (it == 0) LQ_TS(1);
           after_chunk(it);
         }
@@ -684,6 +753,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
         for (int s = 0; s < 4; ++s)
 #pragma unroll
           for (int g = 0; g < G; ++g) bc[s][g] = bn[s][g];
+        if constexpr (CVT) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) scc[g] = scn[g];
+        }
       }
     }
   } else {
@@ -697,7 +770,15 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
         if (it < n_it) {
           const uint8_t* tab[T];
           tables(tab);
-          compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
+          if constexpr (CVT) {
+            float scs[G];
+            chunk_scales(scs, it & 1);
+            clear_c();
+            compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], accc, r, t, tab);
+            fold_c(scs);
+          } else {
+            compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
+          }
           if (it == 0) LQ_TS(1);
           after_chunk(it);
         }
@@ -772,10 +853,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   flush_trace(p);
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
+template <int G, int WF, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
-  stream_body<G, WF, F16, PAIR, OUTF32, 0>(a, logical_wg(a.P), sm, NoWait{});
+  stream_body<G, WF, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg(a.P), sm, NoWait{});
 }
 
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
@@ -913,20 +994,20 @@ int choose_wgs(long long U) {
   return static_cast<int>(std::max<long long>(P, 1));
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32>
+template <int G, int WF, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g(const StreamArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((stream_kernel<G, WF, F16, PAIR, OUTF32>), dim3(a.P), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((stream_kernel<G, WF, F16, PAIR, OUTF32, CVT>), dim3(a.P), dim3(kThreads), 0, s, a);
   return check_launch("stream_gemm");
 }
 
-template <int WF, bool F16, bool PAIR, bool OUTF32>
+template <int WF, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 int launch_m(const StreamArgs& a, hipStream_t s) {
   switch (cdiv(a.M, 16)) {
-    case 1: return launch_g<1, WF, F16, PAIR, OUTF32>(a, s);
-    case 2: return launch_g<2, WF, F16, PAIR, OUTF32>(a, s);
-    case 3: return launch_g<3, WF, F16, PAIR, OUTF32>(a, s);
-    case 4: return launch_g<4, WF, F16, PAIR, OUTF32>(a, s);
-    default: return launch_g<5, WF, F16, PAIR, OUTF32>(a, s);
+    case 1: return launch_g<1, WF, F16, PAIR, OUTF32, CVT>(a, s);
+    case 2: return launch_g<2, WF, F16, PAIR, OUTF32, CVT>(a, s);
+    case 3: return launch_g<3, WF, F16, PAIR, OUTF32, CVT>(a, s);
+    case 4: return launch_g<4, WF, F16, PAIR, OUTF32, CVT>(a, s);
+    default: return launch_g<5, WF, F16, PAIR, OUTF32, CVT>(a, s);
   }
 }
 
@@ -988,7 +1069,7 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
   a.P = choose_wgs(units);
   if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrices too large for one launch");
   a.U = static_cast<int>(units);
-  if (!pair && fmt != kFp8 && !f16) return fail(LQ_ERR_ARG, nm + ": NVFP4 streams FP16 activations");
+  if (!pair && fmt != kFp8 && !f16 && outf32) return fail(LQ_ERR_ARG, nm + ": BF16 activations with NVFP4 give BF16 out");
   return LQ_OK;
 }
 
@@ -1012,6 +1093,9 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     if (f16) return outf32 ? launch_m<kFp8, true, false, true>(a, s) : launch_m<kFp8, true, false, false>(a, s);
     return outf32 ? launch_m<kFp8, false, false, true>(a, s) : launch_m<kFp8, false, false, false>(a, s);
   }
+  // NVFP4 runs on the FP16 MFMA: BF16 activations are converted chunk by chunk in the kernel
+  if (!f16) return fmt == kFp4 ? launch_m<kFp4, true, false, false, true>(a, s)
+                               : launch_m<kFp4Coded, true, false, false, true>(a, s);
   if (fmt == kFp4) return outf32 ? launch_m<kFp4, true, false, true>(a, s) : launch_m<kFp4, true, false, false>(a, s);
   return outf32 ? launch_m<kFp4Coded, true, false, true>(a, s) : launch_m<kFp4Coded, true, false, false>(a, s);
 }
@@ -1194,16 +1278,9 @@ int lq_stream_ffn_deadline_status(int* hit) {
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
                          int N, int K, void* stream) {
   if (int rc = check_rows("stream_nvfp4_bf16", M, N, K)) return rc;
-  Workspace* ws = workspace_for_current_device();
-  if (!ws) return LQ_ERR_DEVICE;
-  int rc = ws->reserve_half(static_cast<size_t>(M) * K);
-  if (rc) return rc;
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  rc = half_rows(true, x, M, K, ws->xh, ws->xinv, s);
-  if (rc) return rc;
   const Mat m{w, table, nullptr, scale2, y, nullptr, N, N};
-  return stream_launch("stream_nvfp4_bf16", table ? kFp4Coded : kFp4, true, false, false, ws->xh, ws->xinv, M, &m, 1, K,
-                       s);
+  return stream_launch("stream_nvfp4_bf16", table ? kFp4Coded : kFp4, false, false, false, x, nullptr, M, &m, 1, K,
+                       static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

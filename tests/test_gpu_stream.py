@@ -38,13 +38,15 @@ def bf16_host(t: torch.Tensor) -> np.ndarray:
     return t.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def assert_close_bf16(got_bits: np.ndarray, ref_bits: np.ndarray, what: str):
+def assert_close_bf16(got_bits: np.ndarray, ref_bits: np.ndarray, what: str, row_scaled: bool = False):
+    """row_scaled: inputs deliberately scaled far from N(0, 1) per row; the mean absolute error is then taken
+    in units of each row's rms."""
     got = O.bf16_to_f32(got_bits).astype(np.float64)
     ref = O.bf16_to_f32(ref_bits).astype(np.float64)
     assert np.isfinite(got).all(), what
     rms = np.sqrt(np.mean(ref * ref, axis=-1, keepdims=True)) + 1e-30
     rel = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms))
-    mae = np.mean(np.abs(got - ref))
+    mae = np.mean(np.abs(got - ref) / rms) if row_scaled else np.mean(np.abs(got - ref))
     assert rel <= 1e-2, f"{what}: max rel err {rel:.3e}"
     assert mae <= 1e-3, f"{what}: mean abs err {mae:.3e}"
     return rel, mae
@@ -275,14 +277,34 @@ def test_coded_equals_raw_and_multi_equals_separate(L):
 
 
 def test_stream_nvfp4_bf16(L):
+    """BF16 activations on the NVFP4 path: each 128-value chunk of a row is staged as FP16 under its own
+    power-of-two scale. Rows span 1e-6 .. 3e4 in magnitude, chunks within a row differ by up to 2^12, one row is
+    zero; every M is row-invariant against M = 68, raw and coded scales agree."""
     N, K = 512, 2560
     w = O.normal_bf16(16, 0.02, (N, K))
     v, s, g, _ = O.quant_nvfp4(w)
     tw = L.retile_nvfp4(to_dev(v), to_dev(s))
-    x = O.normal_bf16(17, 1.0, (16, K))
+    xf = O.bf16_to_f32(O.normal_bf16(17, 1.0, (68, K))).astype(np.float32)
+    row_scale = np.float32(10.0) ** np.linspace(-6, 4.5, 68).astype(np.float32)
+    chunk_scale = np.float32(2.0) ** ((np.arange(K) // 128) % 13 - 6).astype(np.float32)
+    xf = xf * row_scale[:, None] * chunk_scale[None, :]
+    xf[5] = 0
+    x = O.f32_to_bf16(xf)
     ref = O.f32_to_bf16(O.gemm_f32(O.bf16_to_f32(x), O.dequant_nvfp4(v, s, g)))
-    got = bf16_host(L.stream_nvfp4_bf16(bf16_dev(x), tw, None, g, N))
-    assert_close_bf16(got, ref, "nvfp4 bf16")
+    full = bf16_host(L.stream_nvfp4_bf16(bf16_dev(x), tw, None, g, N))
+    assert_close_bf16(full, ref, "nvfp4 bf16 M=68", row_scaled=True)
+    assert not full[5].any()
+    xs = O.normal_bf16(18, 1.0, (16, K))
+    ref16 = O.f32_to_bf16(O.gemm_f32(O.bf16_to_f32(xs), O.dequant_nvfp4(v, s, g)))
+    assert_close_bf16(bf16_host(L.stream_nvfp4_bf16(bf16_dev(xs), tw, None, g, N)), ref16, "nvfp4 bf16 N(0,1)")
+    for M in [1, 16, 17, 33]:
+        got = bf16_host(L.stream_nvfp4_bf16(bf16_dev(x[:M]), tw, None, g, N))
+        assert np.array_equal(got, full[:M]), f"nvfp4 bf16 row invariance M={M}"
+    ok, table, code_of = O.scale_code_table(s)
+    assert ok
+    twc, _ = L.retile_nvfp4_coded(to_dev(v), to_dev(s), to_dev(code_of))
+    coded = bf16_host(L.stream_nvfp4_bf16(bf16_dev(x), twc, to_dev(table), g, N))
+    assert np.array_equal(coded, full)
 
 
 def test_error_paths(L):
