@@ -39,10 +39,14 @@ constexpr int kRowBytes = 128;                   // one K block of one row (FP8)
 constexpr int kOpBytes = 256 * kRowBytes;        // one operand's K block in LDS: 32 KB
 constexpr int kStage = 2 * kOpBytes + kBM * 4;   // weights, activations, activation scales: 65 KB
 
-// Byte offset of 16-byte unit u of row `row` in an LDS operand tile.
-// A fragment read serves 16 lanes (rows r .. r + 15, one unit each) per 256-byte LDS cycle: bank group
-// (row % 2) * 8 + swizzled unit is then distinct across the 16 rows.
-__device__ __forceinline__ int lds_off(int row, int u) { return row * kRowBytes + ((u ^ ((row >> 1) & 7)) << 4); }
+// Byte offset of 16-byte unit u of row `row` in an LDS operand tile: the unit index is XOR-swizzled by
+// swz(row). A fragment read has 16 lanes reading one unit each of rows r .. r + 15 (r % 16 == 0). swz makes
+// every aligned group of 8 rows hit 8 distinct units (8 lanes x 16 bytes cover the 32 banks once) and every
+// group of 16 rows hit distinct (row parity, unit) pairs (16 lanes cover 64 banks once), so the reads are
+// conflict free whether the LDS serves 8 or 16 lanes of a 16-byte read per cycle (measured: no bank
+// conflicts; the former swizzle by row / 2 had them on half of all LDS cycles).
+__device__ __forceinline__ int swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+__device__ __forceinline__ int lds_off(int row, int u) { return row * kRowBytes + ((u ^ swz(row)) << 4); }
 
 struct PrefillArgs {
   const uint8_t* xq;
@@ -98,11 +102,11 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.xs), 0, a.M * a.KB * 4, 0x00020000);
 
   // Load-to-LDS plan: load i (0..3) of wave w writes LDS bytes [((i * 8 + w) * 64 + lane) * 16, +16) of an
-  // operand tile: row = (i * 8 + w) * 8 + lane / 8, swizzled unit lane % 8, i.e. source unit u = lane % 8 ^ (row / 2 % 8)
+  // operand tile: row = (i * 8 + w) * 8 + lane / 8, swizzled unit lane % 8, i.e. source unit u = lane % 8 ^ swz(row)
   // (the same for every i, as i moves the row by 64). Weights: the row's 16-row tile tw and row rr in it; unit
   // u = 2 tt + q sits at tiled piece ((h*2 + q)*8 + g)*4 + tt (g = rr % 8, h = rr / 8); load i is 4 tiles on.
-  // Activations: row-major, load i is 64 rows on. The per-i and per-block steps go in the scalar offset.
-  const int row0 = wave * 8 + (lane >> 3), u0 = (lane & 7) ^ ((row0 >> 1) & 7);
+  // Activations: row-major, load i is 64 rows on (a multiple of 16 rows: swz is the same). The per-i and per-block steps go in the scalar offset.
+  const int row0 = wave * 8 + (lane >> 3), u0 = (lane & 7) ^ swz(row0);
   const int wsrc = (((n0 >> 4) + (row0 >> 4)) * a.KB) * kTileBytesFp8 +
                    (((((row0 & 15) >> 3) * 2 + (u0 & 1)) * 8 + (row0 & 7)) * 4 + (u0 >> 1)) * 16;
   const int xsrc = (m0 + row0) * a.K + u0 * 16;
