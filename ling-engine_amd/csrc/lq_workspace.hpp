@@ -1,5 +1,6 @@
 // Per-device workspace of the skinny GEMMs: split-K partial sums, per-tile-group arrival counters (kept
-// zero between launches: the last workgroup of a group resets its counter) and the one-launch FFN's counters.
+// zero between launches: the last workgroup of a group resets its counter), the one-launch FFN's counters and
+// the prefill GEMM's split-tile partials.
 // Grow-only; allocated on first use or by lq_init().
 #pragma once
 
@@ -13,9 +14,15 @@ struct Workspace {
   size_t partial_bytes = 0;
   int* counters = nullptr;
   size_t counter_count = 0;
-  int* sync = nullptr;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
+  int* sync = nullptr;
+  // prefill tail split: FP32 partial tiles and per-tile arrival counters (zeroed once, self-resetting)
+  float* pf_partials = nullptr;
+  size_t pf_partial_bytes = 0;
+  int* pf_counters = nullptr;
+  size_t pf_counter_count = 0;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
   // Ensure capacity; returns LQ_OK or LQ_ERR_DEVICE (message set).
   int reserve_stream(size_t partial_bytes_needed, size_t counters_needed);
+  int reserve_prefill(size_t partial_bytes_needed, size_t counters_needed);
 };
 
 // The calling thread's current device's workspace (created on first call), or null (error set).

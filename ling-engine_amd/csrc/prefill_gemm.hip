@@ -24,6 +24,7 @@
 //    token tile per group), so the workgroups running at once on an XCD share the K slices of both operands
 //    in its L2 instead of re-streaming the whole activation matrix per weight tile.
 #include "lq_common.hpp"
+#include "lq_workspace.hpp"
 
 #include <algorithm>
 #include <string>
@@ -35,6 +36,7 @@ constexpr int kBN = 256;  // weight rows per workgroup
 constexpr int kBM = 256;  // tokens per workgroup
 constexpr int kThreads = 512;
 constexpr int kGroupN = 4;                       // weight tiles per raster group
+constexpr int kMaxSplit = 4;                     // K parts of a tail tile
 constexpr int kRowBytes = 128;                   // one K block of one row (FP8)
 constexpr int kOpBytes = 256 * kRowBytes;        // one operand's K block in LDS: 32 KB
 constexpr int kStage = 2 * kOpBytes + kBM * 4;   // weights, activations, activation scales: 65 KB
@@ -57,6 +59,12 @@ struct PrefillArgs {
   void* y;          // BF16 or FP32 [M][ldy]
   int ldy, M, N, K, KB;
   int tiles_m, tiles_n;
+  // Tail split: tiles [full, full + rem) of the logical order are each computed by S workgroups over
+  // consecutive K ranges; their FP32 partials meet in part[(rt * S + p) * kBN * kBM] and the last part to
+  // arrive (counter cnt[rt]) adds them in part order and writes the tile.
+  int full, rem, S;
+  float* part;
+  int* cnt;
 };
 
 // Output of a prefill GEMM: BF16, FP32, or FP32 added to what y holds.
@@ -87,9 +95,21 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   // Tile order. The hardware places block b on XCD b % 8; each XCD takes a contiguous range of the logical
   // tile order, in which tiles come in groups of kGroupN weight tiles x all token tiles, token tile slowest
   // within a group.
-  const int nb = gridDim.x, b = blockIdx.x;
-  int tile = b;
-  if ((nb & 7) == 0) tile = (b & 7) * (nb >> 3) + (b >> 3);
+  // Split workgroups come after the whole tiles (the hardware dispatches in order, so they fill the last,
+  // partial round); the S parts of a tile are on one XCD (same blockIdx % 8), sharing its L2.
+  const int b = blockIdx.x;
+  int tile = b, kb0 = 0, kb1 = a.KB, part = -1, rt = 0;
+  if (b < a.full) {
+    if ((a.full & 7) == 0) tile = (b & 7) * (a.full >> 3) + (b >> 3);
+  } else {
+    const int sidx = b - a.full, q = sidx >> 3;
+    rt = (q / a.S) * 8 + (sidx & 7);
+    part = q % a.S;
+    if (rt >= a.rem) return;
+    tile = a.full + rt;
+    kb0 = part * a.KB / a.S;
+    kb1 = (part + 1) * a.KB / a.S;
+  }
   const int grp = tile / (kGroupN * a.tiles_m), rem = tile % (kGroupN * a.tiles_m);
   const int gsize = min(kGroupN, a.tiles_n - grp * kGroupN);
   const int tn = grp * kGroupN + rem % gsize, tm = rem / gsize;
@@ -175,21 +195,21 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
       for (int v = 0; v < 4; ++v) dst[j][v] = __builtin_fmaf(p[j][v], s[j], dst[j][v]);
   };
 
-  issue(0, 0);
+  issue(0, kb0);
   LQ_WAIT_VM0();
   __builtin_amdgcn_s_barrier();
-  block_start(0, 0);
+  block_start(0, kb0);
   // Per K block and weight tile: the tile's four MFMAs, then the next tile's fragment read, then the fold of
   // the four results into the accumulators (the other wave on the SIMD issues its MFMAs meanwhile). The one
   // barrier per block sits after tile 7's MFMAs are issued: it publishes the next block's loads and frees this
   // block's stage for its refill. Empty volatile statements pin this order (the compiler would otherwise sink
   // the MFMAs to their use, hoist the reads and defer the folds, and run out of registers).
-  for (int kb = 0; kb < a.KB; ++kb) {
-    const int st = kb & 1;
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int st = (kb - kb0) & 1;
     const uint8_t* sa = smem + st * kStage;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      if (i < 5 && kb + 1 < a.KB) issue_part(st ^ 1, kb + 1, i);
+      if (i < 5 && kb + 1 < kb1) issue_part(st ^ 1, kb + 1, i);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         // E8M0 scale 127 = 1.0 on both operands: the plain FP8 x FP8 product of one 128-value block
@@ -217,7 +237,55 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
         asm volatile("" ::"v"(acc[i][0]), "v"(acc[i][1]), "v"(acc[i][2]), "v"(acc[i][3]));
       }
     }
-    if (kb + 1 < a.KB) block_start(st ^ 1, kb + 1);
+    if (kb + 1 < kb1) block_start(st ^ 1, kb + 1);
+  }
+
+  if (part >= 0) {
+    // A split tile: publish this part (agent-coherent stores: vector v = i * 4 + j of thread tid at
+    // (v * kThreads + tid) * 16 bytes), count the arrival; the last part adds all parts in order.
+    __shared__ int last_part;
+    constexpr int kTileBytes = kBN * kBM * 4;
+    const __amdgpu_buffer_rsrc_t pr_rs =
+        __builtin_amdgcn_make_buffer_rsrc(a.part + static_cast<size_t>(rt) * a.S * (kBN * kBM), 0, a.S * kTileBytes,
+                                          0x00020000);
+    const int own = part * kTileBytes + static_cast<int>(threadIdx.x) * 16;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[i][j], pr_rs, own + (i * 4 + j) * kThreads * 16, 0, 16 /* sc1 */);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const int old = __hip_atomic_fetch_add(a.cnt + rt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_part = old == a.S - 1;
+      if (last_part) __hip_atomic_store(a.cnt + rt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_part) return;
+    // sum over parts 0 .. S-1 in order, one weight tile (4 vectors x S parts) per batch of loads; this
+    // workgroup's own part is in its registers
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      f32x4 pv[kMaxSplit][4];
+#pragma unroll
+      for (int p = 0; p < kMaxSplit; ++p)
+        if (p < a.S && p != part)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            pv[p][j] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           pr_rs, p * kTileBytes + static_cast<int>(threadIdx.x) * 16 + (i * 4 + j) * kThreads * 16,
+                           0, 16 /* sc1 */));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4 sum = part == 0 ? acc[i][j] : pv[0][j];
+#pragma unroll
+        for (int p = 1; p < kMaxSplit; ++p)
+          if (p < a.S) sum = sum + (p == part ? acc[i][j] : pv[p][j]);
+        acc[i][j] = sum;
+      }
+    }
   }
 
   // epilogue: lane holds rows n = n0 + wn*128 + 16i + 4t + v, token m = m0 + wm*64 + 16j + r
@@ -306,7 +374,31 @@ int prefill_launch(PrefillArgs a, const char* name, hipStream_t s) {
   a.KB = a.K / 128;
   a.tiles_m = cdiv(a.M, kBM);
   a.tiles_n = cdiv(a.N, kBN);
-  const long long blocks = static_cast<long long>(a.tiles_m) * a.tiles_n;
+  const long long tiles = static_cast<long long>(a.tiles_m) * a.tiles_n;
+  // Tail split: when the tiles leave the last round of one-tile-per-CU workgroups at most a third full, the
+  // tiles of that round are each split along K into S parts (S <= #CUs / rem, each part >= 8 K blocks, S <= 4).
+  // Measured on config 4: down (64 of 256 CUs busy in the last round, S = 4) gains 8%; a half-full last round
+  // (gate|up, S would be 2) loses 4% to the partial traffic, as the clock rises when CUs idle.
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const long long P = device_cus(dev);
+  a.rem = static_cast<int>(tiles % P);
+  a.S = a.rem ? static_cast<int>(std::min<long long>({P / a.rem, a.KB / 8, kMaxSplit})) : 1;
+  if (a.S < 3) {
+    a.S = 1;
+    a.rem = 0;
+  }
+  a.full = static_cast<int>(tiles - a.rem);
+  const long long blocks = a.full + (a.rem ? 8LL * cdiv(a.rem, 8) * a.S : 0);
+  if (a.rem) {
+    Workspace* ws = workspace_for_current_device();
+    if (!ws) return LQ_ERR_DEVICE;
+    const int rc = ws->reserve_prefill(static_cast<size_t>(a.rem) * a.S * kBN * kBM * sizeof(float),
+                                       static_cast<size_t>(a.rem));
+    if (rc) return rc;
+    a.part = ws->pf_partials;
+    a.cnt = ws->pf_counters;
+  }
   // 130 KB of dynamic LDS is above the default per-launch limit; raise it (once per instantiation).
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_fp8_kernel<BLOCK, OUT>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, 2 * kStage);

@@ -80,6 +80,29 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
   return LQ_OK;
 }
 
+int Workspace::reserve_prefill(size_t bytes, size_t counters_needed) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  if (bytes > pf_partial_bytes) {
+    if (pf_partials) (void)hipFree(pf_partials);
+    pf_partials = nullptr;
+    pf_partial_bytes = 0;
+    if (hipMalloc(&pf_partials, bytes) != hipSuccess)
+      return fail(LQ_ERR_DEVICE, "workspace: prefill partial buffer allocation failed");
+    pf_partial_bytes = bytes;
+  }
+  if (counters_needed > pf_counter_count) {
+    const size_t cap = std::max(counters_needed, size_t(4096));
+    if (pf_counters) (void)hipFree(pf_counters);
+    pf_counters = nullptr;
+    pf_counter_count = 0;
+    if (hipMalloc(&pf_counters, cap * sizeof(int)) != hipSuccess ||
+        hipMemset(pf_counters, 0, cap * sizeof(int)) != hipSuccess)
+      return fail(LQ_ERR_DEVICE, "workspace: prefill counter allocation failed");
+    pf_counter_count = cap;
+  }
+  return LQ_OK;
+}
+
 }  // namespace lq
 
 extern "C" {

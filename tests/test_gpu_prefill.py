@@ -66,12 +66,17 @@ def prefill_case(L, M, N, K, seed):
     return wq, ws, xq, xs, tw
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (130, 256, 384), (512, 384, 1024), (257, 128, 2048)])
+# (300, 256, 4096) and (257, 128, 3072): every tile is split along K into 4 / 3 parts (the tail split)
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (130, 256, 384), (512, 384, 1024), (257, 128, 3072),
+                                   (300, 256, 4096)])
 def test_prefill_small_full(L, M, N, K):
     wq, ws, xq, xs, tw = prefill_case(L, M, N, K, 50 + M)
     y = L.prefill_fp8_block(to_dev(xq), to_dev(xs), tw, to_dev(ws), N)
     ref = O.prefill_fp8_rows(xq, xs, np.arange(M), wq, ws)
     check(bf16_host(y), ref, f"prefill M={M} N={N} K={K}")
+    # split tiles add their parts in a fixed order: a second launch is bit-identical
+    y2 = L.prefill_fp8_block(to_dev(xq), to_dev(xs), tw, to_dev(ws), N)
+    assert np.array_equal(bf16_host(y), bf16_host(y2))
 
 
 def test_prefill_stray_columns_and_rows(L):
@@ -158,7 +163,7 @@ def check_f32(got, ref_abs, what, base=None):
     assert rel <= 2e-3, f"{what}: max rel {rel:.3e}"
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (200, 384, 640), (513, 256, 1024)])
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (200, 384, 640), (513, 256, 1024), (300, 256, 4096)])
 def test_prefill_per_tensor_f32_and_accumulate(L, M, N, K):
     wq, xq, tw = pt_case(L, M, N, K, 70 + M)
     alpha = 3.0e-4
