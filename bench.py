@@ -38,6 +38,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma list of extra sections to run (default: all)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--vendor-reference", action="store_true",
+                    help="also time hipBLASLt's per-tensor FP8 GEMM (torch._scaled_mm) on the config-4 shapes, for comparison")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB device copy (the known-size kernel that scales HBM byte counters)")
     return ap.parse_args()
@@ -294,6 +296,26 @@ def bench_prefill(torch, L, O, args, dev):
         del w, a, xs, y
     res["total"] = {"flop": total_flop, "ms": total_ms, "tflops": total_flop / (total_ms * 1e-3) / 1e12,
                     "frac_mfma": total_flop / (total_ms * 1e-3) / 1e12 / FP8_DENSE_TFLOPS}
+    if args.vendor_reference:
+        # a comparison point only (not this library's path): the vendor GEMM with one scale per tensor
+        ref = {}
+        for name, N, K in (("gate_up", 2 * F, H), ("down", H, F)):
+            a = torch.randn(M, K, device=dev).to(torch.float8_e4m3fn)
+            b = torch.randn(N, K, device=dev).to(torch.float8_e4m3fn)
+            one = torch.tensor(1.0, device=dev)
+            for _ in range(3):
+                torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(10):
+                torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
+            t1.record()
+            torch.cuda.synchronize()
+            ms = t0.elapsed_time(t1) / 10
+            ref[name] = {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+            del a, b
+        res["hipblaslt_fp8_per_tensor"] = ref
     torch.cuda.empty_cache()
     return res
 
