@@ -134,6 +134,19 @@ int lq_stream_ffn_deadline_status(int* hit);
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
                          int N, int K, void* stream);
 
+/* ---------------- prefill activation producers (reference src/core/kernels.cuh:190-206) ---------------- */
+/* x [M][K] FP32 -> NVFP4: q packed [M][K/2] (low nibble first), E4M3 block scales sf [M][K/16], global scale
+ * 1 / input_scale; each value rounded to BF16 first. K % 16 == 0. kernels.cuh:193 quant_act_nvfp4. */
+int lq_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf, void* stream);
+/* The same for silu(g) * u (silu(v) = v / (1 + e^-v)). kernels.cuh:195-196 silu_mul_quant_nvfp4. */
+int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float input_scale, uint8_t* q, uint8_t* sf,
+                            void* stream);
+/* Gemma RMSNorm of each row, v = x * rstd * (1 + w) with rstd = 1 / sqrt(mean(x^2) + eps), into `out` (FP32,
+ * may be null) and straight into the next GEMM's encoding: NVFP4 (q [M][H/2], sf [M][H/16]) when nvfp4, else FP8
+ * E4M3(BF16(v) / input_scale) saturated (q [M][H]). H % 1024 == 0. kernels.cuh:203-204 rmsnorm_quant. */
+int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
+                     float input_scale, uint8_t* q, uint8_t* sf, void* stream);
+
 /* ---------------- prefill, block-scaled FP8 (additive; reference src/core/kernels.cuh:190-221) ---------------- */
 /* BF16 x [M][K] -> FP8 E4M3 q [M][K] with one FP32 scale per 1x128 group, scale [M][K/128] = amax / 448 (1 for an
  * all-zero group), q = E4M3_rne(x / scale). The block-scaled counterpart of quant_act_fp8 (kernels.cuh:199). */

@@ -106,6 +106,19 @@ inline void stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const 
   lq_check(lq_stream_nvfp4_bf16(x, M, w, table, scale2, y, N, K, s));
 }
 
+// ---- prefill activation producers (kernels.cuh:190-206) ----
+inline void quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf, hipStream_t s) {
+  lq_check(lq_quant_act_nvfp4(x, M, K, input_scale, q, sf, s));
+}
+inline void silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float input_scale, uint8_t* q,
+                                 uint8_t* sf, hipStream_t s) {
+  lq_check(lq_silu_mul_quant_nvfp4(g, u, M, K, input_scale, q, sf, s));
+}
+inline void rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, bool nvfp4,
+                          float input_scale, uint8_t* q, uint8_t* sf, hipStream_t s) {
+  lq_check(lq_rmsnorm_quant(x, w, out, M, H, eps, nvfp4 ? 1 : 0, input_scale, q, sf, s));
+}
+
 // ---- prefill (block-scaled FP8; kernels.cuh:190-221 for the reference's per-tensor forms) ----
 inline void quant_act_fp8_g128(const uint16_t* x_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t s) {
   lq_check(lq_quant_act_fp8_g128(x_bf16, M, K, q, scale, s));

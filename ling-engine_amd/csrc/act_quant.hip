@@ -1,0 +1,172 @@
+// Activation producers of the prefill GEMMs, fused with their quantization (reference
+// src/core/prefill_gemm.cu:378-459, 607-637): the NVFP4 activation quantizer, the same on silu(g) * u, and the
+// Gemma RMSNorm straight into FP8 or NVFP4. Every value is rounded to BF16 first (production's activations are
+// BF16), as the reference does.
+//
+// NVFP4 (reference put_nvfp4, prefill_gemm.cu:382-394): per block of 16 consecutive values along K,
+//   g = 1 / input_scale, sc = E4M3_rne_satfinite(g * (amax * (1/6))), os = sv != 0 ? 1 / (sv * (1/g)) : 0
+//   (sv = the E4M3 value of sc), codes = E2M1 round-to-nearest-even, saturating, sign kept (a small negative
+//   value gives code 8), low nibble first.
+// One thread per 16-value block: 64 bytes in, 9 bytes out; consecutive threads read consecutive blocks.
+#include "lq_common.hpp"
+
+#include <string>
+
+namespace lq {
+namespace {
+
+// E2M1 nearest, ties to the even code (values 0, .5, 1, 1.5, 2, 3, 4, 6): each term counts a midpoint passed,
+// strictly above it when the lower code is the even one, from it when the upper one is.
+__device__ __forceinline__ uint32_t e2m1_rne(float y) {
+  const float a = fabsf(y);
+  uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.f);
+  if (isnan(a)) c = 7;
+  return c | (signbit(y) ? 8u : 0u);
+}
+
+// E4M3, round to nearest even, saturating to +-448 (NaN stays NaN).
+__device__ __forceinline__ uint32_t e4m3_sat(float v) {
+  return __builtin_amdgcn_cvt_pk_fp8_f32(isnan(v) ? v : fminf(fmaxf(v, -448.f), 448.f), 0.f, 0, false) & 0xffu;
+}
+
+__device__ __forceinline__ float bf16_round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+__device__ __forceinline__ float silu_ref(float x) { return x / (1.f + __expf(-x)); }
+
+// Block b's 16 values (already BF16-rounded) -> 8 code bytes and the scale byte.
+__device__ __forceinline__ void put_nvfp4_block(const float (&v)[16], float g, uint8_t* q8, uint8_t* sfb) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const uint32_t sc = e4m3_sat(g * (amax * (1.f / 6.f)));
+  const float sv = e4m3_to_f32(sc);
+  const float os = sv != 0.f ? 1.f / (sv * (1.f / g)) : 0.f;
+  uint32_t w[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 16; i += 2) {
+    const uint32_t byte = e2m1_rne(v[i] * os) | (e2m1_rne(v[i + 1] * os) << 4);
+    w[i >> 3] |= byte << (8 * ((i >> 1) & 3));
+  }
+  *reinterpret_cast<u32x2*>(q8) = u32x2{w[0], w[1]};
+  *sfb = static_cast<uint8_t>(sc);
+}
+
+template <bool SILU>
+__global__ void __launch_bounds__(256) quant_nvfp4_kernel(const float* __restrict__ x, const float* __restrict__ u,
+                                                          size_t blocks, float g, uint8_t* __restrict__ q,
+                                                          uint8_t* __restrict__ sf) {
+  for (size_t b = blockIdx.x * static_cast<size_t>(256) + threadIdx.x; b < blocks;
+       b += static_cast<size_t>(gridDim.x) * 256) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 f = reinterpret_cast<const f32x4*>(x)[b * 4 + k];
+      f32x4 uu = f32x4{1.f, 1.f, 1.f, 1.f};
+      if constexpr (SILU) uu = reinterpret_cast<const f32x4*>(u)[b * 4 + k];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[4 * k + e] = bf16_round(SILU ? silu_ref(f[e]) * uu[e] : f[e]);
+    }
+    put_nvfp4_block(v, g, q + b * 8, sf + b);
+  }
+}
+
+// One workgroup per row: the sum of squares (each thread's float4 slices, then the wave and the four waves
+// in a fixed order), rstd = 1 / sqrt(sum / H + eps), v = x * rstd * (1 + w) (written to `out` when given),
+// then each thread quantizes whole 16-value blocks of BF16(v): NVFP4, or FP8 E4M3(BF16(v) / input_scale).
+template <bool FP4>
+__global__ void __launch_bounds__(256) rmsnorm_quant_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                            float* __restrict__ out, int H, float eps, float g,
+                                                            uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
+  __shared__ float red[4];
+  const size_t r = blockIdx.x;
+  const float* row = x + r * H;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H / 4; i += 256) {
+    const f32x4 f = reinterpret_cast<const f32x4*>(row)[i];
+    ss = __builtin_fmaf(f[0], f[0], ss);
+    ss = __builtin_fmaf(f[1], f[1], ss);
+    ss = __builtin_fmaf(f[2], f[2], ss);
+    ss = __builtin_fmaf(f[3], f[3], ss);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rstd = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+  for (int blk = threadIdx.x; blk < H / 16; blk += 256) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 f = reinterpret_cast<const f32x4*>(row)[blk * 4 + k];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int h = blk * 16 + 4 * k + e;
+        v[4 * k + e] = f[e] * rstd * (1.f + bf16_to_f32(w[h]));
+      }
+      if (out) reinterpret_cast<f32x4*>(out + r * H)[blk * 4 + k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = bf16_round(v[i]);
+    const size_t b = r * (H / 16) + blk;
+    if constexpr (FP4) {
+      put_nvfp4_block(v, g, q + b * 8, sf + b);
+    } else {
+      uint32_t wq[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        wq[k] = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) wq[k] |= e4m3_sat(v[4 * k + e] * g) << (8 * e);
+      }
+      reinterpret_cast<u32x4*>(q)[b] = u32x4{wq[0], wq[1], wq[2], wq[3]};
+    }
+  }
+}
+
+unsigned grid_for(size_t items) {
+  const size_t b = (items + 255) / 256;
+  return static_cast<unsigned>(b < 8192 ? (b ? b : 1) : 8192);
+}
+
+}  // namespace
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+int lq_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
+  if (M < 1 || K <= 0 || K % 16 != 0) return fail(LQ_ERR_SHAPE, "quant_act_nvfp4: M >= 1 and K % 16 == 0");
+  if (!x || !q || !sf) return fail(LQ_ERR_ARG, "quant_act_nvfp4: null pointer");
+  const size_t blocks = static_cast<size_t>(M) * K / 16;
+  hipLaunchKernelGGL(quant_nvfp4_kernel<false>, dim3(grid_for(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                     nullptr, blocks, 1.f / input_scale, q, sf);
+  return check_launch("quant_act_nvfp4");
+}
+
+int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float input_scale, uint8_t* q, uint8_t* sf,
+                            void* stream) {
+  if (M < 1 || K <= 0 || K % 16 != 0) return fail(LQ_ERR_SHAPE, "silu_mul_quant_nvfp4: M >= 1 and K % 16 == 0");
+  if (!g || !u || !q || !sf) return fail(LQ_ERR_ARG, "silu_mul_quant_nvfp4: null pointer");
+  const size_t blocks = static_cast<size_t>(M) * K / 16;
+  hipLaunchKernelGGL(quant_nvfp4_kernel<true>, dim3(grid_for(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), g,
+                     u, blocks, 1.f / input_scale, q, sf);
+  return check_launch("silu_mul_quant_nvfp4");
+}
+
+int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
+                     float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
+  if (M < 1) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: M must be positive");
+  if (H <= 0 || H % 1024 != 0) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: H % 1024 must be 0");
+  if (!x || !w || !q || (nvfp4 && !sf)) return fail(LQ_ERR_ARG, "rmsnorm_quant: null pointer");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (nvfp4)
+    hipLaunchKernelGGL(rmsnorm_quant_kernel<true>, dim3(M), dim3(256), 0, s, x, w, out, H, eps, 1.f / input_scale, q, sf);
+  else
+    hipLaunchKernelGGL(rmsnorm_quant_kernel<false>, dim3(M), dim3(256), 0, s, x, w, out, H, eps, 1.f / input_scale, q,
+                       nullptr);
+  return check_launch("rmsnorm_quant");
+}
+
+}  // extern "C"

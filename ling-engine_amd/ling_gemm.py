@@ -44,6 +44,9 @@ SIGNATURES = {
     "lq_stream_ffn_deadline_status": (_I, [_P]),
     "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_quant_act_fp8_g128": (_I, [_P, _I, _I, _P, _P, _P]),
+    "lq_quant_act_nvfp4": (_I, [_P, _I, _I, _F, _P, _P, _P]),
+    "lq_silu_mul_quant_nvfp4": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
+    "lq_rmsnorm_quant": (_I, [_P, _P, _P, _I, _I, _F, _I, _F, _P, _P, _P]),
     "lq_prefill_fp8_block": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
     "lq_rmsnorm_half": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _I, _P]),
     "lq_quant_act_fp8": (_I, [_P, _I, _I, _F, _P, _P]),
@@ -282,6 +285,35 @@ def stream_nvfp4_bf16(x, w, table, scale2: float, N: int, y=None):
     _check(lib.lq_stream_nvfp4_bf16(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(table), scale2, _ptr(y), N, K,
                                     _stream()))
     return y
+
+
+# ---------------- prefill activation producers ----------------
+def quant_act_nvfp4(x, input_scale: float):
+    M, K = x.shape
+    q = torch.empty((M, K // 2), dtype=torch.uint8, device=x.device)
+    sf = torch.empty((M, K // 16), dtype=torch.uint8, device=x.device)
+    _check(lib.lq_quant_act_nvfp4(_ptr(_dev(x, torch.float32)), M, K, input_scale, _ptr(q), _ptr(sf), _stream()))
+    return q, sf
+
+
+def silu_mul_quant_nvfp4(g, u, input_scale: float):
+    M, K = g.shape
+    q = torch.empty((M, K // 2), dtype=torch.uint8, device=g.device)
+    sf = torch.empty((M, K // 16), dtype=torch.uint8, device=g.device)
+    _check(lib.lq_silu_mul_quant_nvfp4(_ptr(_dev(g, torch.float32)), _ptr(_dev(u, torch.float32)), M, K, input_scale,
+                                       _ptr(q), _ptr(sf), _stream()))
+    return q, sf
+
+
+def rmsnorm_quant(x, w_bf16, eps: float, nvfp4: bool, input_scale: float, with_out: bool = True):
+    """-> (out FP32 or None, q, sf or None)."""
+    M, H = x.shape
+    out = torch.empty((M, H), dtype=torch.float32, device=x.device) if with_out else None
+    q = torch.empty((M, H // 2) if nvfp4 else (M, H), dtype=torch.uint8, device=x.device)
+    sf = torch.empty((M, H // 16), dtype=torch.uint8, device=x.device) if nvfp4 else None
+    _check(lib.lq_rmsnorm_quant(_ptr(_dev(x, torch.float32)), _ptr(_dev(w_bf16)), _ptr(out), M, H, eps, int(nvfp4),
+                                input_scale, _ptr(q), _ptr(sf), _stream()))
+    return out, q, sf
 
 
 # ---------------- prefill ----------------

@@ -432,6 +432,70 @@ void or_quant_act_fp8(const float* x, size_t n, float input_scale, uint8_t* q) {
   for (size_t i = 0; i < n; ++i) q[i] = or_e4m3_encode(or_bf16_float(or_bf16_bits(x[i])) * inv);
 }
 
+/* NVFP4 activation block (reference put_nvfp4, src/core/prefill_gemm.cu:382-394; the host restatement the
+ * reference's own test checks the device against, tests/prefill_tests.cu:71-80): 16 values already rounded to
+ * BF16, g = 1 / input_scale; sc = E4M3(g * (amax * (1/6))), os = sv != 0 ? 1 / (sv * (1/g)) : 0, codes =
+ * E2M1 RNE (ties to the even code, saturating, sign kept) of v * os, low nibble first. */
+static void nvfp4_act_block(const float* v, float g, uint8_t* q8, uint8_t* sfb) {
+  float amax = 0.f;
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  const uint8_t sc = or_e4m3_encode(g * (amax * (1.f / 6.f)));
+  const float sv = or_e4m3_decode(sc);
+  const float os = sv != 0.f ? 1.f / (sv * (1.f / g)) : 0.f;
+  for (int i = 0; i < 16; i += 2)
+    q8[i / 2] = (uint8_t)(or_e2m1_encode_rne(v[i] * os) | (or_e2m1_encode_rne(v[i + 1] * os) << 4));
+  *sfb = sc;
+}
+
+/* quant_act_nvfp4 (reference src/core/prefill_gemm.cu:404-420, 607-611): x [M][K] FP32 -> q [M][K/2], sf [M][K/16]. */
+void or_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf) {
+  const float g = 1.f / input_scale;
+  const size_t blocks = (size_t)M * K / 16;
+  for (size_t b = 0; b < blocks; ++b) {
+    float v[16];
+    for (int i = 0; i < 16; ++i) v[i] = or_bf16_float(or_bf16_bits(x[b * 16 + i]));
+    nvfp4_act_block(v, g, q + b * 8, sf + b);
+  }
+}
+
+/* silu_mul_quant_nvfp4 (reference prefill_gemm.cu:404-420 with SILU, 613-618): the values are silu(g) * u. */
+void or_silu_mul_quant_nvfp4(const float* gt, const float* u, int M, int K, float input_scale, uint8_t* q, uint8_t* sf) {
+  const float g = 1.f / input_scale;
+  const size_t blocks = (size_t)M * K / 16;
+  for (size_t b = 0; b < blocks; ++b) {
+    float v[16];
+    for (int i = 0; i < 16; ++i) v[i] = or_bf16_float(or_bf16_bits(or_silu(gt[b * 16 + i]) * u[b * 16 + i]));
+    nvfp4_act_block(v, g, q + b * 8, sf + b);
+  }
+}
+
+/* rmsnorm_quant (reference norm_quant_kernel, prefill_gemm.cu:426-459, 632-637): Gemma RMSNorm of each row,
+ * v = x * rstd * (1 + w), rstd = 1 / sqrt(sum(x^2) / H + eps) (the sum in double here), into `out` when given,
+ * then BF16(v) into NVFP4 or FP8 E4M3(BF16(v) * (1 / input_scale)) saturated. */
+void or_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
+                      float input_scale, uint8_t* q, uint8_t* sf) {
+  const float g = 1.f / input_scale;
+  float* v = (float*)malloc(sizeof(float) * (size_t)H);
+  for (int r = 0; r < M; ++r) {
+    const float* row = x + (size_t)r * H;
+    double ss = 0.0;
+    for (int h = 0; h < H; ++h) ss += (double)row[h] * row[h];
+    const float rstd = 1.f / sqrtf((float)(ss / H) + eps);
+    for (int h = 0; h < H; ++h) {
+      v[h] = row[h] * rstd * (1.f + or_bf16_float(w[h]));
+      if (out) out[(size_t)r * H + h] = v[h];
+      v[h] = or_bf16_float(or_bf16_bits(v[h]));
+    }
+    if (nvfp4) {
+      for (int b = 0; b < H / 16; ++b)
+        nvfp4_act_block(v + b * 16, g, q + ((size_t)r * H / 16 + b) * 8, sf + (size_t)r * H / 16 + b);
+    } else {
+      for (int h = 0; h < H; ++h) q[(size_t)r * H + h] = or_e4m3_encode(v[h] * g);
+    }
+  }
+  free(v);
+}
+
 /* ------------------------------------------------------------------------------------------------ */
 /* reference GEMM                                                                                     */
 /* ------------------------------------------------------------------------------------------------ */

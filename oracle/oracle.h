@@ -115,6 +115,11 @@ void or_rmsnorm_half(const float* x, const uint16_t* w, int rows, int H, float e
                      uint16_t* xh, float* xinv);
 /* Per-tensor FP8 activations: E4M3_satfinite(bf16(x) * (1 / input_scale)). */
 void or_quant_act_fp8(const float* x, size_t n, float input_scale, uint8_t* q);
+/* prefill activation producers (reference src/core/prefill_gemm.cu:382-459, 607-637) */
+void or_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf);
+void or_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float input_scale, uint8_t* q, uint8_t* sf);
+void or_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
+                      float input_scale, uint8_t* q, uint8_t* sf);
 
 int or_hardware_threads(void);
 

@@ -63,6 +63,9 @@ def _load():
         "or_prefill_fp8_rows": (None, [P, P, P, i, P, P, i, i, P, i]),
         "or_rmsnorm_half": (None, [P, P, i, i, f, i, P, P, P]),
         "or_quant_act_fp8": (None, [P, sz, f, P]),
+        "or_quant_act_nvfp4": (None, [P, i, i, f, P, P]),
+        "or_silu_mul_quant_nvfp4": (None, [P, P, i, i, f, P, P]),
+        "or_rmsnorm_quant": (None, [P, P, P, i, i, f, i, f, P, P]),
         "or_hardware_threads": (i, []),
     }
     for name, (res, args) in sig.items():
@@ -282,6 +285,38 @@ def quant_act_fp8(x: np.ndarray, input_scale: float) -> np.ndarray:
     q = np.empty(x.shape, np.uint8)
     lib.or_quant_act_fp8(_p(x), x.size, input_scale, _p(q))
     return q
+
+
+def quant_act_nvfp4(x: np.ndarray, input_scale: float):
+    """x FP32 [M][K] -> (q [M][K/2] packed E2M1, sf [M][K/16] E4M3) (reference prefill_gemm.cu:382-420)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, K = x.shape
+    q = np.empty((M, K // 2), np.uint8)
+    sf = np.empty((M, K // 16), np.uint8)
+    lib.or_quant_act_nvfp4(_p(x), M, K, input_scale, _p(q), _p(sf))
+    return q, sf
+
+
+def silu_mul_quant_nvfp4(g: np.ndarray, u: np.ndarray, input_scale: float):
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    M, K = g.shape
+    q = np.empty((M, K // 2), np.uint8)
+    sf = np.empty((M, K // 16), np.uint8)
+    lib.or_silu_mul_quant_nvfp4(_p(g), _p(u), M, K, input_scale, _p(q), _p(sf))
+    return q, sf
+
+
+def rmsnorm_quant(x: np.ndarray, w_bf16: np.ndarray, eps: float, nvfp4: bool, input_scale: float):
+    """-> (out FP32 [M][H], q, sf or None) (reference prefill_gemm.cu:426-459)."""
+    x = np.ascontiguousarray(x, np.float32)
+    M, H = x.shape
+    out = np.empty((M, H), np.float32)
+    q = np.empty((M, H // 2) if nvfp4 else (M, H), np.uint8)
+    sf = np.empty((M, H // 16), np.uint8) if nvfp4 else None
+    lib.or_rmsnorm_quant(_p(x), _p(np.ascontiguousarray(w_bf16, np.uint16)), _p(out), M, H, eps, int(nvfp4),
+                         input_scale, _p(q), _p(sf) if sf is not None else None)
+    return out, q, sf
 
 
 def hardware_threads() -> int:

@@ -210,3 +210,67 @@ def test_rmsnorm_half(L, rows, H, gemma):
     ch, ci = O.to_half_rows(o)
     assert np.array_equal(xh.view(torch.int16).cpu().numpy().view(np.uint16), ch)
     assert np.array_equal(xinv.cpu().numpy(), ci)
+
+
+# ---------------- activation producers (reference prefill_gemm.cu:382-459, 607-637) ----------------
+def _reference_test_activations(M, K, seed):
+    """The reference's own test distribution (tests/prefill_tests.cu:58-60): N(0, 1) * 0.003, every 97th value
+    40 times larger."""
+    x = O.normal_f32(seed, 1.0, (M, K)).reshape(-1)
+    x[::97] *= 40.0
+    return (x * 0.003).astype(np.float32).reshape(M, K)
+
+
+@pytest.mark.parametrize("M,K", [(67, 512), (5, 5120), (1, 16)])
+def test_quant_act_nvfp4_bit_exact(L, M, K):
+    x = _reference_test_activations(M, K, 21 + M)
+    in4 = 0.0019763766  # the reference test's input scale
+    q, sf = L.quant_act_nvfp4(to_dev(x), in4)
+    rq, rsf = O.quant_act_nvfp4(x, in4)
+    assert np.array_equal(sf.cpu().numpy(), rsf), "scales"
+    assert np.array_equal(q.cpu().numpy(), rq), "codes"
+
+
+def test_silu_mul_quant_nvfp4(L):
+    """silu(g) * u into NVFP4. The device exp and the oracle's libm expf may round silu differently in the last
+    bit, which can move a value across a BF16 rounding boundary: at most a few codes in 10^3 may differ, and
+    the scales must agree except where such a value is a block's largest."""
+    M, K = 17, 4096
+    g = O.normal_f32(31, 2.0, (M, K))
+    u = O.normal_f32(32, 1.0, (M, K))
+    q, sf = L.silu_mul_quant_nvfp4(to_dev(g), to_dev(u), 0.01)
+    rq, rsf = O.silu_mul_quant_nvfp4(g, u, 0.01)
+    qd, sfd = q.cpu().numpy(), sf.cpu().numpy()
+    assert np.mean(sfd != rsf) <= 1e-3
+    assert np.mean(qd != rq) <= 3e-3
+
+
+@pytest.mark.parametrize("nvfp4", [False, True])
+def test_rmsnorm_quant(L, nvfp4):
+    M, H = 5, 5120
+    x = O.normal_f32(41, 3.0, (M, H))
+    w = O.normal_bf16(42, 0.2, (H,))
+    scale = 0.01 if nvfp4 else 0.02
+    out, q, sf = L.rmsnorm_quant(to_dev(x), to_dev(w.view(np.int16)), 1e-6, nvfp4, scale)
+    ref_out, _, _ = O.rmsnorm_quant(x, w, 1e-6, nvfp4, scale)
+    outd = out.cpu().numpy()
+    assert np.max(np.abs(outd - ref_out)) <= 4e-6 * np.max(np.abs(ref_out))  # FP32 rounding of the norm
+    # the quantization of the kernel's own FP32 output is byte for byte the oracle's quantizer
+    if nvfp4:
+        rq, rsf = O.quant_act_nvfp4(outd, scale)
+        assert np.array_equal(sf.cpu().numpy(), rsf)
+    else:
+        rq = O.quant_act_fp8(outd, scale)
+    assert np.array_equal(q.cpu().numpy(), rq)
+    # without the FP32 copy the bytes are the same
+    _, q2, sf2 = L.rmsnorm_quant(to_dev(x), to_dev(w.view(np.int16)), 1e-6, nvfp4, scale, with_out=False)
+    assert np.array_equal(q2.cpu().numpy(), q.cpu().numpy())
+
+
+def test_activation_producer_errors(L):
+    x = torch.zeros((2, 24), dtype=torch.float32, device=DEV)
+    with pytest.raises(L.LingGemmError, match="K % 16"):
+        L.quant_act_nvfp4(x, 1.0)
+    w = torch.zeros((1000,), dtype=torch.int16, device=DEV)
+    with pytest.raises(L.LingGemmError, match="H % 1024 must be 0"):
+        L.rmsnorm_quant(torch.zeros((1, 1000), dtype=torch.float32, device=DEV), w, 1e-6, True, 1.0)

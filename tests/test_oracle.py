@@ -294,3 +294,59 @@ def test_quant_act_fp8_per_tensor_vs_torch():
     xb = torch.from_numpy(x).to(torch.bfloat16).float() * (1.0 / np.float32(s))
     ref = xb.clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
     assert np.array_equal(q, ref)
+
+
+# ---------------- prefill activation producers (reference src/core/prefill_gemm.cu:382-459) ----------------
+def test_quant_act_nvfp4_known_answers():
+    """A block with amax 6 at input_scale 1 has scale E4M3(1.0) = 0x38 and os = 1, so each code is the E2M1
+    round-to-nearest-even of the value itself: every midpoint goes to the even code, a small negative value keeps
+    its sign (code 8), low nibble first."""
+    v = np.array([[6, -6, 3, 0.1, -0.1, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, -5, 0, -0.0, 0.26]], np.float32)
+    q, sf = O.quant_act_nvfp4(v, 1.0)
+    assert sf[0, 0] == 0x38
+    assert list(q[0]) == [0xF7, 0x05, 0x08, 0x22, 0x44, 0x66, 0x0E, 0x18]
+    # a zero block: scale 0 and os 0, codes 0 (8 for negative zero)
+    z = np.zeros((1, 16), np.float32)
+    z[0, 1] = -0.0
+    q, sf = O.quant_act_nvfp4(z, 1.0)
+    assert sf[0, 0] == 0 and list(q[0]) == [0x80] + [0] * 7
+    # saturating scale: g * amax / 6 above 448 gives 0x7e (448) and the largest value's code 7 or less
+    big = np.full((1, 16), 1e6, np.float32)
+    q, sf = O.quant_act_nvfp4(big, 1.0)
+    assert sf[0, 0] == 0x7E and all(b == 0x77 for b in q[0])
+    # input_scale divides: x * (1 / input_scale) scaled blocks give the scale of the unscaled block
+    x = O.bf16_to_f32(O.normal_bf16(5, 1.0, (4, 64)))
+    q1, s1 = O.quant_act_nvfp4(x, 1.0)
+    q2, s2 = O.quant_act_nvfp4(x * 4, 4.0)
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+def test_quant_act_nvfp4_block_error_band():
+    """Each dequantized value e2m1 * (sv / g) is within half an E2M1 step of the value (round to nearest), with
+    the scale from the block's largest magnitude: relative error of the block's largest values below 1/6."""
+    x = O.bf16_to_f32(O.normal_bf16(9, 1.0, (8, 256))).astype(np.float32)
+    q, sf = O.quant_act_nvfp4(x, 0.5)
+    g = 1.0 / 0.5
+    codes = np.stack([q & 15, q >> 4], axis=-1).reshape(x.shape)
+    vals = np.array([O.lib.or_e2m1_decode(int(c)) for c in codes.reshape(-1)], np.float64).reshape(x.shape)
+    sv = np.array([O.lib.or_e4m3_decode(int(b)) for b in sf.reshape(-1)], np.float64).reshape(8, 16)
+    deq = vals * np.repeat(sv, 16, axis=1) / g
+    step = np.repeat(sv, 16, axis=1) / g  # one unit of E2M1 at scale 1 is 0.5 .. 2 wide: bound by the largest step
+    assert np.all(np.abs(deq - x) <= 1.0 * step + 1e-12)
+    amax = np.abs(x).reshape(8, 16, 16).max(axis=2)
+    assert np.all(np.abs(sv * 6 / g - amax) <= amax / 16 + 1e-12)  # the scale itself: E4M3 of amax / 6
+
+
+def test_rmsnorm_quant_oracle_consistency():
+    """rmsnorm_quant = Gemma RMSNorm, then the quantizers on its output (FP8: quant_act_fp8; NVFP4:
+    quant_act_nvfp4), byte for byte."""
+    x = O.normal_f32(11, 1.0, (3, 1024))
+    w = O.normal_bf16(12, 0.1, (1024,))
+    out, q8, _ = O.rmsnorm_quant(x, w, 1e-6, False, 0.05)
+    assert np.array_equal(q8, O.quant_act_fp8(out, 0.05))
+    out4, q4, sf4 = O.rmsnorm_quant(x, w, 1e-6, True, 0.01)
+    qq, ss = O.quant_act_nvfp4(out4, 0.01)
+    assert np.array_equal(out, out4) and np.array_equal(q4, qq) and np.array_equal(sf4, ss)
+    ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2, axis=1, keepdims=True) + 1e-6)
+    ref *= 1.0 + O.bf16_to_f32(w).astype(np.float64)
+    assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
