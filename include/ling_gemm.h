@@ -104,6 +104,15 @@ typedef struct {
 int lq_stream_gemm_multi(int nvfp4, const uint16_t* xh, const float* xinv, int M, const lq_stream_target* t, int n,
                          int K, void* stream);
 
+/* The sparse head: y[M][cap] = scale2 * xh . W[rows[i]]^T * xinv for i < *nrows (device count), -inf after; W the
+ * tiled NVFP4 blob of the full matrix of N rows (raw: raw_scales null; coded: raw_scales = its raw scales, 128 B
+ * per block). Each element's arithmetic is the full stream_gemm_nvfp4 launch's over the same blob, so a selected
+ * row's logit is bit for bit the full head's. cap % 32 == 0. N is an addition to the reference's arguments: the
+ * full launch's split of K depends on it here. kernels.cuh:294-295 stream_gemm_gather_nvfp4. */
+int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, const uint8_t* w,
+                                const uint8_t* raw_scales, float scale2, const int* rows, const int* nrows, int cap,
+                                float* y, int K, int N, void* stream);
+
 /* ---------------- rows path, BF16 formats (additive; per-channel FP8 scales, BF16 in and out) ---------------- */
 /* y[M][N] = bf16(wscale_n[n] * x . W^T), W tiled FP8, x BF16 [M][K]. Replaces the engine's linear_fp8
  * (reference src/core/engine.cpp:1272-1281) for per-channel checkpoints. */

@@ -83,6 +83,12 @@ inline void stream_gemm_multi(bool nvfp4, const __half* x, const float* xinv, in
   lq_check(lq_stream_gemm_multi(nvfp4 ? 1 : 0, reinterpret_cast<const uint16_t*>(x), xinv, M, c, n, K, s));
 }
 
+inline void stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, const uint8_t* w,
+                                     const uint8_t* raw_scales, float scale2, const int* rows, const int* nrows,
+                                     int cap, float* y, int K, int N, hipStream_t s) {
+  lq_check(lq_stream_gemm_gather_nvfp4(xh, xinv, M, w, raw_scales, scale2, rows, nrows, cap, y, K, N, s));
+}
+
 // ---- rows path, BF16 formats (additive) ----
 inline void stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N, int K,
                           hipStream_t s) {

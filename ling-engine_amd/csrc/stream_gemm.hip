@@ -900,6 +900,144 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
   }
 }
 
+// ---------------- gathered rows (reference stream_gemm_gather_nvfp4, src/core/stream_gemm.cu:1902-1923) -------------
+// y[m][i] = scale2 * x[m] . W[rows[i]] * xinv[m] for i < *nrows, -inf for nrows <= i < cap, with every element's
+// arithmetic that of the full NVFP4 launch over all N rows (so a selected row's logit is bit for bit the full
+// head's): the same 16 value bytes and 2 scale bytes per chunk (a coded blob's raw-scale copy holds exactly the
+// bytes its codes stand for), the same MFMA steps in chunk order, the accumulator cut where the full launch's
+// stream-K split cuts that row's tile group (workgroup boundaries of the full launch's P and units), and the
+// segments added left to right as its finisher adds them. A wave computes 16 gathered rows; a lane's four
+// output rows may belong to different tile groups, so each keeps its own next cut.
+struct GatherArgs {
+  const void* x;      // FP16 [M][K]
+  const float* xinv;  // [M]
+  int M, K, C;
+  const uint8_t* w;    // tiled NVFP4 blob (raw: 1152 B blocks; coded: 1024 B value blocks)
+  const uint8_t* raw;  // coded blob's raw scales (128 B per block), or null for a raw blob
+  float scale2;
+  const int* rows;
+  const int* nrows;
+  int cap, N;        // N: the full matrix's rows
+  int P, U, TGR;     // the full launch's workgroups, units and rows per tile group
+  float* y;          // [M][cap]
+};
+
+template <int G>
+__global__ void __launch_bounds__(kThreads) gather_kernel(const GatherArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[16 * G * 256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, t = lane >> 4;
+  const int cnt = min(max(*a.nrows, 0), a.cap);
+  const int i0 = (blockIdx.x * kWaves + wave) * 16;  // this wave's first gathered row
+  const bool any = static_cast<int>(blockIdx.x) * kWaves * 16 < cnt;  // uniform over the workgroup
+  // epilogue rows of this lane: gathered i = i0 + 4t + v, token 16g + r
+  auto store = [&](const float (&val)[G][4]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int m = 16 * g + r;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int i = i0 + 4 * t + v;
+        if (i < a.cap) a.y[static_cast<size_t>(m) * a.cap + i] = i < cnt ? val[g][v] : -INFINITY;
+      }
+    }
+  };
+  if (!any) {
+    float ninf[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) ninf[g][v] = -INFINITY;
+    store(ninf);
+    return;
+  }
+  const int blk_bytes = a.raw ? kValueBytesFp4 : kTileBytesFp4;
+  const __amdgpu_buffer_rsrc_t wrs = make_rsrc(a.w);
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(a.raw ? a.raw : a.w);
+  // the lane's A row (loads): gathered row i0 + r; an invalid or unselected row reads as zeros
+  const int ia = i0 + r;
+  const int na = ia < cnt ? a.rows[ia] : -1;
+  const unsigned aoob = (na >= 0 && na < a.N) ? 0u : 0x80000000u;
+  const int nac = aoob ? 0 : na;
+  const int slot = (nac & 15) * 4 + t;
+  // the lane's output rows: their tile groups and next cuts
+  int tgc[4], nb[4];
+  bool first[4];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int io = i0 + 4 * t + v;
+    int no = io < cnt ? a.rows[io] : 0;
+    no = (no >= 0 && no < a.N) ? no : 0;
+    tgc[v] = (no / a.TGR) * a.C;
+    const int p = wg_of_unit(tgc[v], a.P, a.U);
+    nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+    first[v] = true;
+  }
+  // activations: thread's share of a chunk as in the stream kernel
+  const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x);
+  int xsrc[G], xdst[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int q = i * kThreads + static_cast<int>(threadIdx.x), row = q >> 4, u = q & 15;
+    xsrc[i] = row < a.M ? (row * a.K) * 2 + u * 16 : static_cast<int>(0x80000000u);
+    xdst[i] = xs_off(row, u);
+  }
+  f32x4 acc[1][G];
+  float tot[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    acc[0][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tot[g][v] = 0.f;
+  }
+  const uint8_t* const tab[1] = {nullptr};
+  for (int c = 0; c < a.C; ++c) {
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+      *reinterpret_cast<u32x4*>(xs + xdst[i]) = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i]), c * 256, 0));
+    WRegs<kFp4, 1> R;
+    const size_t blk = static_cast<size_t>(nac >> 4) * a.C + c;
+    R.v[0][0] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>((blk * blk_bytes + slot * 16) | aoob), 0, 0));
+    const size_t so = a.raw ? blk * 128 + slot * 2 : blk * kTileBytesFp4 + 1024 + slot * 2;
+    R.sc[0] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, static_cast<int>(so | aoob), 0, 0));
+    __syncthreads();
+    u32x4 b[G];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      read_b<G>(b, xs, s, r, t);
+      mfma_step<kFp4, true, G, 1>(R, s, b, acc, tab);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (c == nb[v]) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          tot[g][v] = first[v] ? acc[0][g][v] : tot[g][v] + acc[0][g][v];
+          acc[0][g][v] = 0.f;
+        }
+        first[v] = false;
+        if (c + 1 < a.C) {
+          const int p = wg_of_unit(tgc[v] + c + 1, a.P, a.U);
+          nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+        }
+      }
+    }
+  }
+  float val[G][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const int m = 16 * g + r;
+    const float xi = m < a.M ? a.xinv[m] : 1.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) val[g][v] = (tot[g][v] * a.scale2) * xi;
+  }
+  store(val);
+}
+
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
 // Grid (M, S): every block finds the row's largest magnitude (a maximum is exact in any order, so all
 // blocks agree) and converts its slice of K: xh = f16_rn(x * 2^(15 - e)), xinv = 2^(e - 15).
@@ -1262,6 +1400,47 @@ int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const 
   const Mat gu[2] = {{w_gate, nullptr, s_gate, 0.f, h, nullptr, I, I}, {w_up, nullptr, s_up, 0.f, h, nullptr, I, I}};
   const Mat dn{w_down, nullptr, s_down, 0.f, y, resid, H, H};
   return ffn_launch("stream_fp8_pc_ffn", x, M, gu, dn, h, static_cast<hipStream_t>(stream));
+}
+
+int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, const uint8_t* w,
+                                const uint8_t* raw_scales, float scale2, const int* rows, const int* nrows, int cap,
+                                float* y, int K, int N, void* stream) {
+  const std::string nm = "stream_gemm_gather";
+  if (K <= 0 || K % kChunk != 0 || cap <= 0 || cap % 32 != 0)
+    return fail(LQ_ERR_SHAPE, nm + ": K % 128 and cap % 32 must be 0");
+  if (M < 1 || M > LQ_MAX_STREAM_ROWS) return fail(LQ_ERR_SHAPE, nm + ": M must be in [1, 80]");
+  if (N <= 0 || N % 16 != 0) return fail(LQ_ERR_SHAPE, nm + ": N % 16 and K % 128 must be 0");
+  if (!xh || !xinv || !w || !rows || !nrows || !y) return fail(LQ_ERR_ARG, nm + ": null pointer");
+  GatherArgs a{};
+  a.x = xh;
+  a.xinv = xinv;
+  a.M = M;
+  a.K = K;
+  a.C = K / kChunk;
+  a.w = w;
+  a.raw = raw_scales;
+  a.scale2 = scale2;
+  a.rows = rows;
+  a.nrows = nrows;
+  a.cap = cap;
+  a.N = N;
+  a.y = y;
+  // the full launch's split (stream_launch for this N, K): tile groups of group_rows(kFp4) rows
+  a.TGR = group_rows(kFp4, false);
+  const long long units = static_cast<long long>(cdiv(N, a.TGR)) * a.C;
+  a.P = choose_wgs(units);
+  if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrix too large");
+  a.U = static_cast<int>(units);
+  const dim3 grid(cdiv(cap / 16, kWaves));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (cdiv(M, 16)) {
+    case 1: hipLaunchKernelGGL(gather_kernel<1>, grid, dim3(kThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(gather_kernel<2>, grid, dim3(kThreads), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(gather_kernel<3>, grid, dim3(kThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(gather_kernel<4>, grid, dim3(kThreads), 0, s, a); break;
+    default: hipLaunchKernelGGL(gather_kernel<5>, grid, dim3(kThreads), 0, s, a); break;
+  }
+  return check_launch("stream_gemm_gather");
 }
 
 int lq_stream_ffn_deadline_status(int* hit) {

@@ -37,6 +37,7 @@ SIGNATURES = {
     "lq_stream_gemm_fp8": (_I, [_P, _P, _I, _P, _F, _P, _I, _I, _P]),
     "lq_stream_gemm_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_stream_gemm_multi": (_I, [_I, _P, _P, _I, _P, _I, _I, _P]),
+    "lq_stream_gemm_gather_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _P, _I, _P, _I, _I, _P]),
     "lq_stream_fp8_pc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_residual": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _P]),
@@ -224,6 +225,16 @@ def stream_gemm_nvfp4(xh, xinv, w, table, scale2: float, N: int, K: int, y=None)
     y = torch.empty((M, N), dtype=torch.float32, device=xh.device) if y is None else y
     _check(lib.lq_stream_gemm_nvfp4(_ptr(_dev(xh, torch.float16)), _ptr(xinv), M, _ptr(w), _ptr(table), scale2,
                                     _ptr(y), N, K, _stream()))
+    return y
+
+
+def stream_gemm_gather_nvfp4(xh, xinv, w, raw_scales, scale2: float, rows, nrows, cap: int, N: int, K: int, y=None):
+    """rows: int32 device [>= count]; nrows: int32 device [1]. Returns y [M][cap] FP32."""
+    M = xh.shape[0]
+    y = torch.empty((M, cap), dtype=torch.float32, device=xh.device) if y is None else y
+    _check(lib.lq_stream_gemm_gather_nvfp4(_ptr(_dev(xh, torch.float16)), _ptr(xinv), M, _ptr(w), _ptr(raw_scales),
+                                           scale2, _ptr(_dev(rows, torch.int32)), _ptr(_dev(nrows, torch.int32)), cap,
+                                           _ptr(y), K, N, _stream()))
     return y
 
 

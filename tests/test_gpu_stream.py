@@ -276,6 +276,35 @@ def test_coded_equals_raw_and_multi_equals_separate(L):
     assert np.array_equal(y1.cpu().numpy(), y8) and np.array_equal(y2.cpu().numpy(), y8)
 
 
+@pytest.mark.parametrize("N,K", [(4096, 2560), (8192, 5120)])
+def test_stream_gemm_gather_nvfp4_bit_exact(L, N, K):
+    """The sparse head (reference tests/stream_tests.cu:271-300): a row subset, not in order, from the raw blob
+    and from the coded blob with its raw scales; each selected row's logits are the full launch's bit for bit,
+    columns past the count are -inf (workgroups wholly past it included), an empty selection is all -inf. The
+    shapes split every tile group across workgroups, so the full launch's cuts are exercised."""
+    w = O.normal_bf16(60 + N, 0.02, (N, K))
+    v, s, g, _ = O.quant_nvfp4(w)
+    ok, table, code_of = O.scale_code_table(s)
+    assert ok
+    raw = L.retile_nvfp4(to_dev(v), to_dev(s))
+    coded, raw_scales = L.retile_nvfp4_coded(to_dev(v), to_dev(s), to_dev(code_of))
+    rows = np.arange(N - 1, -1, -3, dtype=np.int32)
+    cnt = rows.size
+    cap = (cnt + 96 + 31) // 32 * 32
+    drows = to_dev(rows)
+    x = O.normal_f32(61, 1.0, (68, K))
+    for M in [1, 11, 17, 68]:
+        xh, xinv = L.to_half_rows(to_dev(x[:M]))
+        full = L.stream_gemm_nvfp4(xh, xinv, raw, None, g, N, K).cpu().numpy()
+        for c in [cnt, 5, 0]:
+            dcnt = to_dev(np.array([c], np.int32))
+            want = np.full((M, cap), -np.inf, np.float32)
+            want[:, :c] = full[:, rows[:c]]
+            for blob, rs in ((raw, None), (coded, raw_scales)):
+                got = L.stream_gemm_gather_nvfp4(xh, xinv, blob, rs, g, drows, dcnt, cap, N, K).cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"gather M={M} count={c}"
+
+
 def test_stream_nvfp4_bf16(L):
     """BF16 activations on the NVFP4 path: each 128-value chunk of a row is staged as FP16 under its own
     power-of-two scale. Rows span 1e-6 .. 3e4 in magnitude, chunks within a row differ by up to 2^12, one row is
