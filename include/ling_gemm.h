@@ -143,6 +143,20 @@ int lq_stream_ffn_deadline_status(int* hit);
 int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8_t* table, float scale2, uint16_t* y,
                          int N, int K, void* stream);
 
+/* ---------------- prefill, NVFP4 (reference src/core/kernels.cuh:207-221) ---------------- */
+/* y[M][0..N) (rows ldy apart, FP32) = alpha * xq . W^T, or += with accumulate; xq NVFP4 activations [M][K/2] with E4M3
+ * block scales xs [M][K/16]; W the tiled NVFP4 blob (raw; or coded with wsf = its raw scales, 128 B per block).
+ * Both operands are dequantized exactly (E2M1 x E4M3) and multiplied in FP32. N % 128 == 0, K % 128 == 0; M < 1
+ * does nothing. kernels.cuh:210-211 prefill_gemm_nvfp4. */
+int lq_prefill_gemm_nvfp4(const uint8_t* xq, const uint8_t* xs, int M, const uint8_t* w, float alpha, float* y, int ldy,
+                          int N, int K, int accumulate, void* stream, const uint8_t* wsf);
+/* The FFN's gate and up projections into the down projection's input: NVFP4 of BF16(silu(alpha_gate * xq . G^T) *
+ * (alpha_up * xq . U^T)) with global scale 1 / out_input_scale, q_out [M][N/2], sf_out [M][N/16]; gate_sf / up_sf:
+ * raw scales of coded blobs (both or neither). N % 128 == 0, K % 128 == 0. kernels.cuh:217-221 prefill_swiglu_nvfp4. */
+int lq_prefill_swiglu_nvfp4(const uint8_t* xq, const uint8_t* xs, int M, const uint8_t* gate, float alpha_gate,
+                            const uint8_t* up, float alpha_up, int N, int K, float out_input_scale, uint8_t* q_out,
+                            uint8_t* sf_out, void* stream, const uint8_t* gate_sf, const uint8_t* up_sf);
+
 /* ---------------- prefill activation producers (reference src/core/kernels.cuh:190-206) ---------------- */
 /* x [M][K] FP32 -> NVFP4: q packed [M][K/2] (low nibble first), E4M3 block scales sf [M][K/16], global scale
  * 1 / input_scale; each value rounded to BF16 first. K % 16 == 0. kernels.cuh:193 quant_act_nvfp4. */

@@ -112,6 +112,19 @@ inline void stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const 
   lq_check(lq_stream_nvfp4_bf16(x, M, w, table, scale2, y, N, K, s));
 }
 
+// ---- prefill, NVFP4 (kernels.cuh:207-221) ----
+inline void prefill_gemm_nvfp4(const uint8_t* xq, const uint8_t* xs, int M, const uint8_t* w, float alpha, float* y,
+                               int ldy, int N, int K, bool accumulate, hipStream_t s, const uint8_t* wsf = nullptr) {
+  lq_check(lq_prefill_gemm_nvfp4(xq, xs, M, w, alpha, y, ldy, N, K, accumulate ? 1 : 0, s, wsf));
+}
+inline void prefill_swiglu_nvfp4(const uint8_t* xq, const uint8_t* xs, int M, const uint8_t* gate, float alpha_gate,
+                                 const uint8_t* up, float alpha_up, int N, int K, float out_input_scale, uint8_t* q_out,
+                                 uint8_t* sf_out, hipStream_t s, const uint8_t* gate_sf = nullptr,
+                                 const uint8_t* up_sf = nullptr) {
+  lq_check(lq_prefill_swiglu_nvfp4(xq, xs, M, gate, alpha_gate, up, alpha_up, N, K, out_input_scale, q_out, sf_out, s,
+                                   gate_sf, up_sf));
+}
+
 // ---- prefill activation producers (kernels.cuh:190-206) ----
 inline void quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf, hipStream_t s) {
   lq_check(lq_quant_act_nvfp4(x, M, K, input_scale, q, sf, s));

@@ -45,6 +45,8 @@ SIGNATURES = {
     "lq_stream_ffn_deadline_status": (_I, [_P]),
     "lq_stream_nvfp4_bf16": (_I, [_P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_quant_act_fp8_g128": (_I, [_P, _I, _I, _P, _P, _P]),
+    "lq_prefill_gemm_nvfp4": (_I, [_P, _P, _I, _P, _F, _P, _I, _I, _I, _I, _P, _P]),
+    "lq_prefill_swiglu_nvfp4": (_I, [_P, _P, _I, _P, _F, _P, _F, _I, _I, _F, _P, _P, _P, _P, _P]),
     "lq_quant_act_nvfp4": (_I, [_P, _I, _I, _F, _P, _P, _P]),
     "lq_silu_mul_quant_nvfp4": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
     "lq_rmsnorm_quant": (_I, [_P, _P, _P, _I, _I, _F, _I, _F, _P, _P, _P]),
@@ -296,6 +298,30 @@ def stream_nvfp4_bf16(x, w, table, scale2: float, N: int, y=None):
     _check(lib.lq_stream_nvfp4_bf16(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(table), scale2, _ptr(y), N, K,
                                     _stream()))
     return y
+
+
+# ---------------- prefill, NVFP4 ----------------
+def prefill_gemm_nvfp4(xq, xs, w, alpha: float, N: int, y=None, ldy: int | None = None, accumulate: bool = False,
+                       wsf=None):
+    M, K2 = xq.shape
+    K = K2 * 2
+    ldy = N if ldy is None else ldy
+    y = torch.empty((M, ldy), dtype=torch.float32, device=xq.device) if y is None else y
+    _check(lib.lq_prefill_gemm_nvfp4(_ptr(_dev(xq, torch.uint8)), _ptr(_dev(xs, torch.uint8)), M, _ptr(w), alpha,
+                                     _ptr(_dev(y, torch.float32)), ldy, N, K, int(accumulate), _stream(), _ptr(wsf)))
+    return y
+
+
+def prefill_swiglu_nvfp4(xq, xs, gate, alpha_gate: float, up, alpha_up: float, N: int, out_input_scale: float,
+                         gate_sf=None, up_sf=None):
+    M, K2 = xq.shape
+    K = K2 * 2
+    q = torch.empty((M, N // 2), dtype=torch.uint8, device=xq.device)
+    sf = torch.empty((M, N // 16), dtype=torch.uint8, device=xq.device)
+    _check(lib.lq_prefill_swiglu_nvfp4(_ptr(_dev(xq, torch.uint8)), _ptr(_dev(xs, torch.uint8)), M, _ptr(gate),
+                                       alpha_gate, _ptr(up), alpha_up, N, K, out_input_scale, _ptr(q), _ptr(sf),
+                                       _stream(), _ptr(gate_sf), _ptr(up_sf)))
+    return q, sf
 
 
 # ---------------- prefill activation producers ----------------

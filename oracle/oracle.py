@@ -319,5 +319,13 @@ def rmsnorm_quant(x: np.ndarray, w_bf16: np.ndarray, eps: float, nvfp4: bool, in
     return out, q, sf
 
 
+def prefill_nvfp4_rows(xq, xs, rows, wv, ws, alpha: float) -> np.ndarray:
+    """The NVFP4 prefill GEMM (reference prefill_gemm.cu:344-376, 593-603; y = alpha * xq . W^T over the exactly
+    dequantized operands, E2M1 x E4M3 per 16-value block) for the token rows `rows`, in float64."""
+    xd = dequant_nvfp4(np.ascontiguousarray(xq[rows]), np.ascontiguousarray(xs[rows]), 1.0).astype(np.float64)
+    wd = dequant_nvfp4(wv, ws, 1.0).astype(np.float64)
+    return alpha * (xd @ wd.T)
+
+
 def hardware_threads() -> int:
     return lib.or_hardware_threads()

@@ -274,3 +274,85 @@ def test_activation_producer_errors(L):
     w = torch.zeros((1000,), dtype=torch.int16, device=DEV)
     with pytest.raises(L.LingGemmError, match="H % 1024 must be 0"):
         L.rmsnorm_quant(torch.zeros((1, 1000), dtype=torch.float32, device=DEV), w, 1e-6, True, 1.0)
+
+
+# ---------------- NVFP4 prefill (reference prefill_gemm.cu:344-376, 593-704) ----------------
+def _nvfp4_operands(L, M, N, K, seed):
+    w = O.normal_bf16(seed, 0.02, (N, K))
+    wv, ws, g, _ = O.quant_nvfp4(w)
+    x = O.normal_f32(seed + 1, 1.0, (M, K))
+    xq, xs = O.quant_act_nvfp4(x, 0.0625)
+    return wv, ws, xq, xs
+
+
+def check_f32_tight(got, ref, what):
+    """FP32 outputs of exactly dequantized operands (every product exact in FP32): max |err| / max(|ref|, rms(row))
+    <= 1e-5 against the float64 product."""
+    rms = np.sqrt(np.mean(ref * ref, axis=-1, keepdims=True)) + 1e-30
+    rel = np.max(np.abs(got - ref) / np.maximum(np.abs(ref), rms))
+    assert rel <= 1e-5, f"{what}: max rel {rel:.3e}"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 128, 128), (130, 384, 512), (300, 256, 2048), (513, 640, 1024)])
+def test_prefill_nvfp4(L, M, N, K):
+    wv, ws, xq, xs = _nvfp4_operands(L, M, N, K, 80 + M)
+    raw = L.retile_nvfp4(to_dev(wv), to_dev(ws))
+    alpha = 0.37
+    y = L.prefill_gemm_nvfp4(to_dev(xq), to_dev(xs), raw, alpha, N).cpu().numpy()
+    ref = O.prefill_nvfp4_rows(xq, xs, np.arange(M), wv, ws, alpha)
+    check_f32_tight(y.astype(np.float64), ref, f"nvfp4 prefill M={M} N={N} K={K}")
+    # the coded blob with its raw scales gives the same bits
+    ok, table, code_of = O.scale_code_table(ws)
+    if ok:
+        coded, rs = L.retile_nvfp4_coded(to_dev(wv), to_dev(ws), to_dev(code_of))
+        y2 = L.prefill_gemm_nvfp4(to_dev(xq), to_dev(xs), coded, alpha, N, wsf=rs).cpu().numpy()
+        assert np.array_equal(y2, y)
+    # accumulate into rows ldy apart
+    ldy = N + 32
+    base = torch.full((M, ldy), 0.5, dtype=torch.float32, device=DEV)
+    L.prefill_gemm_nvfp4(to_dev(xq), to_dev(xs), raw, alpha, N, y=base, ldy=ldy, accumulate=True)
+    b = base.cpu().numpy()
+    assert np.all(b[:, N:] == 0.5)
+    check_f32_tight(b[:, :N].astype(np.float64), ref + 0.5, "nvfp4 prefill accumulate")
+
+
+def test_prefill_nvfp4_device_quantized_activations(L):
+    """The activations from quant_act_nvfp4 on the GPU, a larger shape, every 16th row checked."""
+    M, N, K = 1024, 2048, 2048
+    w = O.normal_bf16(90, 0.02, (N, K))
+    wv, ws, _, _ = O.quant_nvfp4(w)
+    raw = L.retile_nvfp4(to_dev(wv), to_dev(ws))
+    x = O.normal_f32(91, 1.0, (M, K))
+    xq, xs = L.quant_act_nvfp4(to_dev(x), 0.03)
+    y = L.prefill_gemm_nvfp4(xq, xs, raw, 1.0, N).cpu().numpy()
+    rows = np.arange(0, M, 16)
+    ref = O.prefill_nvfp4_rows(xq.cpu().numpy(), xs.cpu().numpy(), rows, wv, ws, 1.0)
+    check_f32_tight(y[rows].astype(np.float64), ref, "nvfp4 prefill device-quantized")
+
+
+def test_prefill_swiglu_nvfp4(L):
+    """gate|up into the down projection's NVFP4 input. The float64 products rounded to FP32 can differ from the
+    GPU's FP32 sums in the last bit, which may move a value across a BF16 rounding boundary: at most a few codes
+    in 10^3 and scales in 10^3 may differ from the oracle's quantization of the exact products."""
+    M, N, K = 300, 384, 1024
+    gv_, gs_, xq, xs = _nvfp4_operands(L, M, N, K, 95)
+    uw = O.normal_bf16(97, 0.02, (N, K))
+    uv_, us_, _, _ = O.quant_nvfp4(uw)
+    gate = L.retile_nvfp4(to_dev(gv_), to_dev(gs_))
+    up = L.retile_nvfp4(to_dev(uv_), to_dev(us_))
+    ag, au, osc = 0.8, 1.3, 0.05
+    q, sf = L.prefill_swiglu_nvfp4(to_dev(xq), to_dev(xs), gate, ag, up, au, N, osc)
+    g = O.prefill_nvfp4_rows(xq, xs, np.arange(M), gv_, gs_, ag).astype(np.float32)
+    u = O.prefill_nvfp4_rows(xq, xs, np.arange(M), uv_, us_, au).astype(np.float32)
+    rq, rsf = O.silu_mul_quant_nvfp4(g, u, osc)
+    qd, sfd = q.cpu().numpy(), sf.cpu().numpy()
+    assert np.mean(sfd != rsf) <= 1e-3
+    assert np.mean(qd != rq) <= 3e-3
+    # coded blobs with their raw scales give the same bytes
+    ok1, _, c1 = O.scale_code_table(gs_)
+    ok2, _, c2 = O.scale_code_table(us_)
+    if ok1 and ok2:
+        gc, gr = L.retile_nvfp4_coded(to_dev(gv_), to_dev(gs_), to_dev(c1))
+        uc, ur = L.retile_nvfp4_coded(to_dev(uv_), to_dev(us_), to_dev(c2))
+        q2, sf2 = L.prefill_swiglu_nvfp4(to_dev(xq), to_dev(xs), gc, ag, uc, au, N, osc, gate_sf=gr, up_sf=ur)
+        assert np.array_equal(q2.cpu().numpy(), qd) and np.array_equal(sf2.cpu().numpy(), sfd)
