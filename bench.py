@@ -320,6 +320,51 @@ def bench_prefill(torch, L, O, args, dev):
     return res
 
 
+def bench_prefill_nvfp4(torch, L, args, dev):
+    """The NVFP4 prefill GEMM on config 4's gate|up shape (M = 4096, N = 2 x 17408, K = 5120) and the fused SwiGLU
+    form (gate and up, N = 17408 each, into NVFP4): a beside-line, not a BASELINE config (its prefill is FP8)."""
+    M, H, F = 4096, 5120, 17408
+    g = torch.Generator(device=dev)
+    g.manual_seed(11)
+    res = {}
+
+    def blob(N, K):
+        v = torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, device=dev, generator=g)
+        sc = torch.randint(0x28, 0x48, (N, K // 16), dtype=torch.uint8, device=dev, generator=g)
+        t = L.retile_nvfp4(v, sc)
+        del v, sc
+        return t
+
+    xq = torch.randint(0, 256, (M, H // 2), dtype=torch.uint8, device=dev, generator=g)
+    xs = torch.randint(0x28, 0x48, (M, H // 16), dtype=torch.uint8, device=dev, generator=g)
+    steps = max(5, args.steps // 20)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps
+
+    w = blob(2 * F, H)
+    y = torch.empty((M, 2 * F), dtype=torch.float32, device=dev)
+    ms = timed(lambda: L.prefill_gemm_nvfp4(xq, xs, w, 1.0, 2 * F, y=y))
+    flop = 2.0 * M * 2 * F * H
+    res["gemm_gate_up"] = {"M": M, "N": 2 * F, "K": H, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12}
+    del w, y
+    gw, uw = blob(F, H), blob(F, H)
+    ms = timed(lambda: L.prefill_swiglu_nvfp4(xq, xs, gw, 1.0, uw, 1.0, F, 0.05))
+    res["swiglu_gate_up"] = {"M": M, "N": F, "K": H, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12}
+    del gw, uw
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(O):
     """The oracle's whole CPU path (dequantize to FP32, FP32 accumulate in k order, BF16 out) on the headline
     workload's shapes: one verify-MLP pass at M = 17 (gate 5120->17408, up 5120->17408, down 17408->5120), on
@@ -385,6 +430,10 @@ def main():
         if pf:
             extra["prefill_m4096"] = pf
             log(f"[bench] prefill: {pf['total']}")
+    if only is None or "nvfp4prefill" in only:
+        pn = bench_prefill_nvfp4(torch, L, args, dev)
+        extra["prefill_nvfp4_m4096"] = pn
+        log(f"[bench] prefill nvfp4: {pn}")
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
