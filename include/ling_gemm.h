@@ -34,7 +34,8 @@ enum {
   LQ_ERR_SHAPE = 1,  /* a shape the kernels do not take (K % 128, N % 16, M out of range, ...) */
   LQ_ERR_ARG = 2,    /* a null pointer or an invalid argument */
   LQ_ERR_LAUNCH = 3, /* the HIP runtime reported an error at launch */
-  LQ_ERR_DEVICE = 4  /* device query or workspace allocation failed */
+  LQ_ERR_DEVICE = 4, /* device query or workspace allocation failed */
+  LQ_ERR_IO = 5      /* a file is missing, unreadable or not in the expected format */
 };
 
 /* Largest row count of the skinny (stream) GEMMs: 5 groups of 16 (4 sequences x 17 verify rows = 68 fit).
@@ -192,6 +193,69 @@ int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha,
 /* The same rounded to BF16 (never accumulated). kernels.cuh:239-240 prefill_gemm_fp8_bf16out */
 int lq_prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, float alpha, uint16_t* y, int ldy, int N,
                                 int K, void* stream);
+
+/* ---------------- the on-disk kernel-order weight file (host only; no GPU is used) ----------------
+ * The offline step the reference's README names ("ling-compile") and never built: its load path maps the
+ * safetensors checkpoint (src/core/safetensors.hpp:14-52) and retiles every quantized linear on the GPU at each
+ * load (src/core/model.cu:131-186 over kernels.cuh:168-188 retile_*). lq_wfile_compile does that once, on CPU
+ * threads, writing each tiled blob byte-identical to lq_retile_fp8 / lq_retile_nvfp4 / lq_retile_nvfp4_coded
+ * with its scale side tables; loading is then a copy of 4096-byte-aligned sections to device memory.
+ *
+ * Checkpoint tensors recognised per linear `P` (the reference's Model::fp4 / Model::fp8, model.cu:248-277):
+ *   NVFP4: P.weight U8 [N][K/2], P.weight_scale F8_E4M3 [N][K/16], P.weight_scale_2 scalar, P.input_scale
+ *          scalar (optional). Written coded (LQ_WENTRY_NVFP4_CODED) when the matrix has at most 64 distinct
+ *          scale bytes and LQ_WFILE_NO_CODES is not set (the reference's LING_SCALE_CODES default), else raw.
+ *   FP8:   P.weight F8_E4M3 [N][K] with P.weight_scale_inv [ceil(N/128)][ceil(K/128)] (block scales), or
+ *          P.weight_scale as a scalar (per-tensor) or [N] / [N][1] (per-channel); P.input_scale optional.
+ * Scales may be F32, BF16 or F16 in the checkpoint; the file holds FP32. With LQ_WFILE_PASSTHROUGH every
+ * other tensor is copied as is (LQ_WENTRY_RAW). N % 16 == 0 and K % 128 == 0 for every quantized weight. */
+#define LQ_WFILE_NO_CODES 1
+#define LQ_WFILE_PASSTHROUGH 2
+enum { LQ_WENTRY_FP8 = 1, LQ_WENTRY_NVFP4 = 2, LQ_WENTRY_NVFP4_CODED = 3, LQ_WENTRY_RAW = 4 };
+enum { LQ_WSCALE_NONE = 0, LQ_WSCALE_TENSOR = 1, LQ_WSCALE_CHANNEL = 2, LQ_WSCALE_BLOCK128 = 3 };
+#define LQ_WENTRY_HAS_INPUT_SCALE 1
+
+typedef struct lq_wfile lq_wfile;
+typedef struct {
+  const char* name;     /* the linear's prefix (P), or the tensor's name for LQ_WENTRY_RAW */
+  int kind;             /* LQ_WENTRY_* */
+  int scale_kind;       /* FP8: LQ_WSCALE_*; NVFP4: LQ_WSCALE_NONE (block scales live in the blob / aux) */
+  int N, K;             /* logical matrix shape (0 for raw entries) */
+  float weight_scale;   /* FP8 per-tensor weight_scale; NVFP4 weight_scale_2 */
+  float input_scale;    /* when flags & LQ_WENTRY_HAS_INPUT_SCALE */
+  int flags;
+  char dtype[16];       /* checkpoint dtype of the weight ("U8", "F8_E4M3", "BF16", ...) */
+  int ndim;
+  int64_t shape[4];     /* checkpoint shape of the weight */
+  const uint8_t* blob;  /* host-mapped: the tiled weight (raw entries: the tensor's bytes) */
+  size_t blob_bytes;
+  const uint8_t* aux;   /* coded NVFP4: raw scale copy (128 B per block); FP8: FP32 per-channel [N] or block
+                           [ceil(N/128)][ceil(K/128)] scales; else NULL */
+  size_t aux_bytes;
+  const uint8_t* table; /* coded NVFP4: the 64-byte scale-code table; else NULL */
+  size_t table_bytes;
+} lq_wentry;
+
+/* Compile the checkpoint directory (model.safetensors.index.json + shards, or model.safetensors) into
+ * out_path (written to out_path.partial, then renamed). *entries_written may be NULL. No reference
+ * counterpart (the never-built ling-compile). */
+int lq_wfile_compile(const char* checkpoint_dir, const char* out_path, int flags, int* entries_written);
+/* Map a compiled file and check its header, entry table hash and section bounds. */
+int lq_wfile_open(const char* path, lq_wfile** out);
+void lq_wfile_close(lq_wfile* f);
+int lq_wfile_count(const lq_wfile* f);
+/* Index of the entry named `name`, or -1. */
+int lq_wfile_find(const lq_wfile* f, const char* name);
+/* Entry i; its pointers stay valid until lq_wfile_close. */
+int lq_wfile_entry(const lq_wfile* f, int i, lq_wentry* out);
+/* Recompute entry i's section hashes (LQ_ERR_IO on a mismatch). */
+int lq_wfile_verify(const lq_wfile* f, int i);
+/* Host (CPU-thread) retiles, byte-identical to lq_retile_fp8 / lq_retile_nvfp4 / lq_retile_nvfp4_coded;
+ * host pointers. kernels.cuh:168-169,183-184 */
+int lq_host_retile_fp8(const uint8_t* w, uint8_t* out, int N, int K);
+int lq_host_retile_nvfp4(const uint8_t* w, const uint8_t* wscale, uint8_t* out, int N, int K);
+int lq_host_retile_nvfp4_coded(const uint8_t* w, const uint8_t* wscale, const uint8_t* code_of256, uint8_t* out,
+                               uint8_t* raw_scales, int N, int K);
 
 #ifdef __cplusplus
 }

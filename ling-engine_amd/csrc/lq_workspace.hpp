@@ -14,12 +14,12 @@ struct Workspace {
   size_t partial_bytes = 0;
   int* counters = nullptr;
   size_t counter_count = 0;
-  int* sync = nullptr;
+  int* sync = nullptr;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
   // prefill tail split: FP32 partial tiles and per-tile arrival counters (zeroed once, self-resetting)
   float* pf_partials = nullptr;
   size_t pf_partial_bytes = 0;
   int* pf_counters = nullptr;
-  size_t pf_counter_count = 0;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
+  size_t pf_counter_count = 0;
   // Ensure capacity; returns LQ_OK or LQ_ERR_DEVICE (message set).
   int reserve_stream(size_t partial_bytes_needed, size_t counters_needed);
   int reserve_prefill(size_t partial_bytes_needed, size_t counters_needed);

@@ -55,7 +55,31 @@ SIGNATURES = {
     "lq_quant_act_fp8": (_I, [_P, _I, _I, _F, _P, _P]),
     "lq_prefill_gemm_fp8": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _I, _P]),
     "lq_prefill_gemm_fp8_bf16out": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _P]),
+    "lq_wfile_compile": (_I, [C.c_char_p, C.c_char_p, _I, _P]),
+    "lq_wfile_open": (_I, [C.c_char_p, _P]),
+    "lq_wfile_close": (None, [_P]),
+    "lq_wfile_count": (_I, [_P]),
+    "lq_wfile_find": (_I, [_P, C.c_char_p]),
+    "lq_wfile_entry": (_I, [_P, _I, _P]),
+    "lq_wfile_verify": (_I, [_P, _I]),
+    "lq_host_retile_fp8": (_I, [_P, _P, _I, _I]),
+    "lq_host_retile_nvfp4": (_I, [_P, _P, _P, _I, _I]),
+    "lq_host_retile_nvfp4_coded": (_I, [_P, _P, _P, _P, _P, _I, _I]),
 }
+
+# include/ling_gemm.h lq_wentry / lq_wfile flags and kinds
+WFILE_NO_CODES, WFILE_PASSTHROUGH = 1, 2
+WENTRY_FP8, WENTRY_NVFP4, WENTRY_NVFP4_CODED, WENTRY_RAW = 1, 2, 3, 4
+WSCALE_NONE, WSCALE_TENSOR, WSCALE_CHANNEL, WSCALE_BLOCK128 = 0, 1, 2, 3
+WENTRY_HAS_INPUT_SCALE = 1
+
+
+class WEntry(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("kind", C.c_int), ("scale_kind", C.c_int), ("N", C.c_int), ("K", C.c_int),
+                ("weight_scale", C.c_float), ("input_scale", C.c_float), ("flags", C.c_int),
+                ("dtype", C.c_char * 16), ("ndim", C.c_int), ("shape", C.c_int64 * 4),
+                ("blob", C.c_void_p), ("blob_bytes", C.c_size_t), ("aux", C.c_void_p), ("aux_bytes", C.c_size_t),
+                ("table", C.c_void_p), ("table_bytes", C.c_size_t)]
 
 
 class StreamTarget(C.Structure):
@@ -150,6 +174,43 @@ def scale_code_table(scales_host) -> tuple[bool, bytes, bytes]:
     ok = lib.lq_scale_code_table(s.ctypes.data_as(C.c_void_p), s.size, table.ctypes.data_as(C.c_void_p),
                                  code_of.ctypes.data_as(C.c_void_p))
     return bool(ok), table, code_of
+
+
+def _np_ptr(a):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def host_retile_fp8(w_host):
+    """Row-major FP8 codes [N][K] (numpy uint8) -> the tiled blob, on CPU threads (bytes of retile_fp8)."""
+    import numpy as np
+    w = np.ascontiguousarray(w_host, dtype=np.uint8)
+    N, K = w.shape
+    out = np.empty(tiled_bytes_fp8(N, K), np.uint8)
+    _check(lib.lq_host_retile_fp8(_np_ptr(w), _np_ptr(out), N, K))
+    return out
+
+
+def host_retile_nvfp4(values_host, scales_host):
+    import numpy as np
+    v = np.ascontiguousarray(values_host, dtype=np.uint8)
+    sc = np.ascontiguousarray(scales_host, dtype=np.uint8)
+    N, K = v.shape[0], v.shape[1] * 2
+    out = np.empty(tiled_bytes_nvfp4(N, K), np.uint8)
+    _check(lib.lq_host_retile_nvfp4(_np_ptr(v), _np_ptr(sc), _np_ptr(out), N, K))
+    return out
+
+
+def host_retile_nvfp4_coded(values_host, scales_host, code_of):
+    """-> (coded blob, raw scale copy), the bytes of retile_nvfp4_coded."""
+    import numpy as np
+    v = np.ascontiguousarray(values_host, dtype=np.uint8)
+    sc = np.ascontiguousarray(scales_host, dtype=np.uint8)
+    cm = np.ascontiguousarray(code_of, dtype=np.uint8)
+    N, K = v.shape[0], v.shape[1] * 2
+    out = np.empty(tiled_bytes_nvfp4_coded(N, K), np.uint8)
+    raw = np.empty(N * K // 16, np.uint8)
+    _check(lib.lq_host_retile_nvfp4_coded(_np_ptr(v), _np_ptr(sc), _np_ptr(cm), _np_ptr(out), _np_ptr(raw), N, K))
+    return out, raw
 
 
 def retile_nvfp4_coded(values: torch.Tensor, scales: torch.Tensor, code_of: torch.Tensor):
