@@ -386,10 +386,14 @@ class Checkpoint {
       if (!dt || dt->type != Json::kStr || !sh || sh->type != Json::kArr || !off || off->type != Json::kArr ||
           off->arr.size() != 2)
         throw IoError("bad entry " + kv.first + " in " + shard);
+      if (kv.first.empty() || kv.first.find('\0') != std::string::npos) throw IoError("bad tensor name in " + shard);
       Tensor t;
       t.dtype = dt->str;
+      uint64_t numel = 1;
       for (const Json& d : sh->arr) {
         if (d.type != Json::kNum || !d.integral || d.inum < 0) throw IoError("bad shape of " + kv.first);
+        if (__builtin_mul_overflow(numel, static_cast<uint64_t>(d.inum), &numel) || numel > (uint64_t(1) << 48))
+          throw IoError("shape of " + kv.first + " is too large");
         t.shape.push_back(d.inum);
       }
       for (const Json& o : off->arr)
@@ -589,6 +593,9 @@ std::vector<Plan> plan_checkpoint(const Checkpoint& ck, int flags, std::set<std:
     const bool fp8 = w.dtype == "F8_E4M3";
     if (!nvfp4 && !fp8) continue;
     if (w.shape.size() != 2) throw ArgError(name + ": a quantized weight must be 2-D");
+    // N and K are int in the kernels' interface (and K = 2 x the packed NVFP4 width)
+    if (w.shape[0] > (int64_t(1) << 30) || w.shape[1] > (int64_t(1) << 29))
+      throw ArgError(name + ": dimensions too large for the GEMM interface");
     Plan p;
     p.name = prefix;
     Entry& e = p.e;

@@ -299,3 +299,32 @@ def test_cli(ckpt, tmp_path, capsys):
     assert LC.main([d, out, "--list"]) == 0
     text = capsys.readouterr().out
     assert "5 entries" in text and "nvfp4-coded" in text and "block128" in text
+
+
+def test_hostile_headers_fail(tmp_path):
+    out = str(tmp_path / "h.lqw")
+    # an element count that overflows 64 bits, and dimensions past the GEMM interface's int range
+    for i, shape in enumerate([[1 << 40, 1 << 40, 1 << 40], [1 << 31, 128]]):
+        d = str(tmp_path / f"h{i}")
+        os.makedirs(d)
+        hdr = json.dumps({"a.weight": {"dtype": "F8_E4M3", "shape": shape, "data_offsets": [0, 0]},
+                          "a.weight_scale": {"dtype": "F32", "shape": [], "data_offsets": [0, 4]}}).encode()
+        with open(os.path.join(d, "model.safetensors"), "wb") as f:
+            f.write(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 4)
+        with pytest.raises(L.LingGemmError, match="too large|do not match"):
+            LC.compile_checkpoint(d, out)
+    # a NUL inside a tensor name
+    d = str(tmp_path / "nul")
+    os.makedirs(d)
+    hdr = b'{"a\\u0000b.weight":{"dtype":"F8_E4M3","shape":[16,128],"data_offsets":[0,2048]}}'
+    with open(os.path.join(d, "model.safetensors"), "wb") as f:
+        f.write(struct.pack("<Q", len(hdr)) + hdr + b"\0" * 2048)
+    with pytest.raises(L.LingGemmError, match="bad tensor name"):
+        LC.compile_checkpoint(d, out)
+    # a header length past the end of the file
+    d = str(tmp_path / "len")
+    os.makedirs(d)
+    with open(os.path.join(d, "model.safetensors"), "wb") as f:
+        f.write(struct.pack("<Q", 1 << 40) + b"{}")
+    with pytest.raises(L.LingGemmError, match="bad header length"):
+        LC.compile_checkpoint(d, out)
