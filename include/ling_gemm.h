@@ -48,6 +48,17 @@ const char* lq_last_error(void);
 int lq_init(void);
 /* Library version string. */
 const char* lq_version(void);
+/* Bytes of a caller-owned workspace that serves every skinny (stream) GEMM entry point with M <= max_rows on
+ * the current device (0 for max_rows outside [1, 80]). */
+size_t lq_stream_workspace_bytes(int max_rows);
+/* Make buffer (device memory of the current device, 256-byte aligned, `bytes` long) that device's workspace for
+ * the skinny GEMMs: split-K partial sums, arrival counters, the one-launch FFN's flags. The library frees its
+ * own and allocates nothing more for them; a launch that needs more than the buffer holds fails with LQ_ERR_ARG.
+ * buffer = NULL returns to the library's own workspace. Call outside graph capture, with no launch in flight
+ * that uses the current workspace; the buffer must stay allocated while it is set. The reference's split-K
+ * buffer is a function-static grow-only allocation (src/core/stream_gemm.cu:581-590); this is the
+ * caller-provided form of it. The prefill's tail-split scratch stays library-owned. */
+int lq_set_workspace(void* buffer, size_t bytes);
 
 /* ---------------- tiled layout (reference src/core/kernels.cuh:162-188) ---------------- */
 size_t lq_tiled_bytes_fp8(int N, int K);          /* kernels.cuh:167 tiled_bytes_fp8 */

@@ -32,6 +32,9 @@ struct StreamTarget {
 };
 
 // ---- tiled layout (kernels.cuh:162-188) ----
+// The skinny GEMMs' split-K workspace in caller-owned device memory (nullptr: the library's own again).
+inline size_t stream_workspace_bytes(int max_rows) { return lq_stream_workspace_bytes(max_rows); }
+inline void set_workspace(void* buffer, size_t bytes) { lq_check(lq_set_workspace(buffer, bytes)); }
 inline size_t tiled_bytes_nvfp4(int N, int K) { return lq_tiled_bytes_nvfp4(N, K); }
 inline size_t tiled_bytes_fp8(int N, int K) { return lq_tiled_bytes_fp8(N, K); }
 inline size_t tiled_bytes_nvfp4_coded(int N, int K) { return lq_tiled_bytes_nvfp4_coded(N, K); }

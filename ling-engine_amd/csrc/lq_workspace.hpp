@@ -14,7 +14,8 @@ struct Workspace {
   size_t partial_bytes = 0;
   int* counters = nullptr;
   size_t counter_count = 0;
-  int* sync = nullptr;  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
+  int* sync = nullptr;
+  bool external = false;  // partials, counters and sync live in a caller-owned buffer (lq_set_workspace)  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
   // prefill tail split: FP32 partial tiles and per-tile arrival counters (zeroed once, self-resetting)
   float* pf_partials = nullptr;
   size_t pf_partial_bytes = 0;
@@ -23,6 +24,8 @@ struct Workspace {
   // Ensure capacity; returns LQ_OK or LQ_ERR_DEVICE (message set).
   int reserve_stream(size_t partial_bytes_needed, size_t counters_needed);
   int reserve_prefill(size_t partial_bytes_needed, size_t counters_needed);
+  // Use [buf, buf + bytes) for partials, counters and sync (null: back to the library's own); see lq_set_workspace.
+  int set_external(void* buf, size_t bytes);
 };
 
 // The calling thread's current device's workspace (created on first call), or null (error set).

@@ -53,6 +53,13 @@ Workspace* workspace_for_current_device() {
 
 int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
   std::lock_guard<std::mutex> lock(g_mutex);
+  if (external) {
+    if (bytes > partial_bytes || counters_needed > counter_count)
+      return fail(LQ_ERR_ARG, "workspace: the caller's workspace is too small for this launch (" +
+                                  std::to_string(bytes) + " bytes of partial sums and " +
+                                  std::to_string(counters_needed) + " counters needed; see lq_stream_workspace_bytes)");
+    return LQ_OK;
+  }
   if (bytes > partial_bytes) {
     const size_t cap = std::max(bytes, size_t(64) << 20);
     if (partials) (void)hipFree(partials);
@@ -103,6 +110,39 @@ int Workspace::reserve_prefill(size_t bytes, size_t counters_needed) {
   return LQ_OK;
 }
 
+// Caller-owned layout: [0, 256) sync words, [256, 256 + 4 kExtCounters) counters, then the partial sums.
+constexpr size_t kExtCounters = size_t(1) << 16;
+constexpr size_t kExtHead = 256 + 4 * kExtCounters;
+
+int Workspace::set_external(void* buf, size_t bytes) {
+  std::lock_guard<std::mutex> lock(g_mutex);
+  if (buf && (reinterpret_cast<uintptr_t>(buf) % 256 != 0 || bytes < kExtHead + 256 * 1024))
+    return fail(LQ_ERR_ARG, "set_workspace: the buffer must be 256-byte aligned and at least " +
+                                std::to_string(kExtHead + 256 * 1024) + " bytes");
+  if (buf && hipMemset(buf, 0, kExtHead) != hipSuccess)
+    return fail(LQ_ERR_DEVICE, "set_workspace: clearing the counters failed");
+  if (!external) {  // release the library's own buffers (hipFree waits for work that uses them)
+    if (partials) (void)hipFree(partials);
+    if (counters) (void)hipFree(counters);
+    if (sync) (void)hipFree(sync);
+  }
+  partials = nullptr;
+  counters = nullptr;
+  sync = nullptr;
+  partial_bytes = 0;
+  counter_count = 0;
+  external = buf != nullptr;
+  if (external) {
+    uint8_t* b = static_cast<uint8_t*>(buf);
+    sync = reinterpret_cast<int*>(b);
+    counters = reinterpret_cast<int*>(b + 256);
+    counter_count = kExtCounters;
+    partials = reinterpret_cast<float*>(b + kExtHead);
+    partial_bytes = bytes - kExtHead;
+  }
+  return LQ_OK;
+}
+
 }  // namespace lq
 
 extern "C" {
@@ -111,10 +151,27 @@ const char* lq_last_error(void) { return lq::g_error.c_str(); }
 
 const char* lq_version(void) { return "ling-gemm-mi355x 0.1 (gfx950)"; }
 
+size_t lq_stream_workspace_bytes(int max_rows) {
+  if (max_rows < 1 || max_rows > LQ_MAX_STREAM_ROWS) return 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  const size_t P = static_cast<size_t>(lq::device_cus(dev));
+  const size_t G = static_cast<size_t>((max_rows + 15) / 16);
+  // two slots per workgroup of at most 4 tiles x G groups x 4 floats x 256 threads (the one-launch FFN's two
+  // phases at 2 tiles each take the same)
+  return lq::kExtHead + 2 * P * 4 * G * 4 * 256 * sizeof(float);
+}
+
+int lq_set_workspace(void* buffer, size_t bytes) {
+  lq::Workspace* ws = lq::workspace_for_current_device();
+  if (!ws) return LQ_ERR_DEVICE;
+  return ws->set_external(buffer, bytes);
+}
+
 int lq_init(void) {
   lq::Workspace* ws = lq::workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  int rc = ws->reserve_stream(size_t(64) << 20, size_t(1) << 16);
+  int rc = ws->external ? LQ_OK : ws->reserve_stream(size_t(64) << 20, size_t(1) << 16);
   if (rc) return rc;
   return hipDeviceSynchronize() == hipSuccess ? LQ_OK : lq::fail(LQ_ERR_DEVICE, "lq_init: device synchronize failed");
 }

@@ -21,6 +21,8 @@ SIGNATURES = {
     "lq_last_error": (C.c_char_p, []),
     "lq_init": (_I, []),
     "lq_version": (C.c_char_p, []),
+    "lq_stream_workspace_bytes": (_SZ, [_I]),
+    "lq_set_workspace": (_I, [_P, _SZ]),
     "lq_tiled_bytes_fp8": (_SZ, [_I, _I]),
     "lq_tiled_bytes_nvfp4": (_SZ, [_I, _I]),
     "lq_tiled_bytes_nvfp4_coded": (_SZ, [_I, _I]),
@@ -134,6 +136,18 @@ def _dev(t: torch.Tensor, dtype=None) -> torch.Tensor:
 
 def init() -> None:
     _check(lib.lq_init())
+
+
+def stream_workspace_bytes(max_rows: int = MAX_STREAM_ROWS) -> int:
+    return lib.lq_stream_workspace_bytes(max_rows)
+
+
+def set_workspace(buf) -> None:
+    """buf: a uint8 device tensor that stays alive while set (None: back to the library's own workspace)."""
+    if buf is None:
+        _check(lib.lq_set_workspace(None, 0))
+    else:
+        _check(lib.lq_set_workspace(_ptr(_dev(buf, torch.uint8)), buf.numel()))
 
 
 # ---------------- layout ----------------

@@ -346,3 +346,42 @@ def test_error_paths(L):
         L.stream_fp8_pc(bf16_dev(O.normal_bf16(1, 1.0, (2, 100))), tw, to_dev(s), 16)
     with pytest.raises(L.LingGemmError, match="N % 16"):
         L.stream_fp8_pc(x[:2].contiguous(), tw, to_dev(s), 24)
+
+
+def test_caller_workspace(L):
+    """A caller-owned workspace gives the same bits as the library's own; too small a buffer is an error."""
+    N, K, I = 1024, 2048, 2048
+    q, s = fp8_weights(71, N, K)
+    qg, sg = fp8_weights(72, I, K)
+    qu, su = fp8_weights(73, I, K)
+    qd, sd = fp8_weights(74, K, I)
+    tw, tg, tu, td = (L.retile_fp8(to_dev(a)) for a in (q, qg, qu, qd))
+    sdev = [to_dev(a) for a in (s, sg, su, sd)]
+    x = bf16_dev(O.f32_to_bf16(O.normal_f32(75, 1.0, (68, K))))
+    r = bf16_dev(O.f32_to_bf16(O.normal_f32(76, 1.0, (68, K))))
+
+    def run():
+        y = L.stream_fp8_pc(x, tw, sdev[0], N)
+        h = L.stream_fp8_pc_silu_mul(x, tg, sdev[1], tu, sdev[2], I)
+        h2, out = L.stream_fp8_pc_ffn(x, tg, sdev[1], tu, sdev[2], td, sdev[3], r, I)
+        torch.cuda.synchronize()
+        return [t.view(torch.int16).cpu() for t in (y, h, h2, out)]
+
+    own = run()
+    nbytes = L.stream_workspace_bytes(68)
+    assert nbytes > 0
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    try:
+        L.set_workspace(buf)
+        got = run()
+        assert all(torch.equal(a, b) for a, b in zip(own, got))
+        small = torch.empty(2 << 20, dtype=torch.uint8, device=DEV)
+        L.set_workspace(small)
+        with pytest.raises(L.LingGemmError, match="too small"):
+            L.stream_fp8_pc(x, tw, sdev[0], N)
+        with pytest.raises(L.LingGemmError, match="aligned and at least"):
+            L.set_workspace(small[:1024])
+    finally:
+        L.set_workspace(None)
+    torch.cuda.synchronize()
+    assert all(torch.equal(a, b) for a, b in zip(own, run()))
