@@ -52,6 +52,28 @@ def build() -> dict:
     y = O.prefill_fp8_rows(xq, xs, np.arange(4), wq, ws)
     v["prefill"] = {"x_bf16": hexa(xp), "w_f32_seed": 0x4C51F004, "xq": hexa(xq), "xs": hexa(xs), "wq": hexa(wq),
                     "ws": hexa(ws), "y_f32": hexa(y)}
+    # coded NVFP4 blob (6-bit scale codes) of the same weights
+    ok, table, code_of = O.scale_code_table(sc)
+    blob, raw = O.retile_nvfp4_coded(vals, sc, code_of)
+    v["nvfp4_coded"] = {"ok": ok, "table": hexa(table), "blob": hexa(blob), "raw": hexa(raw)}
+    # activation producers: NVFP4 quantizer, silu(g)*u into NVFP4, Gemma RMSNorm into FP8 and NVFP4
+    xa = O.normal_f32(0x4C51F006, 1.0, (2, 64))
+    xu = O.normal_f32(0x4C51F007, 1.0, (2, 64))
+    qa, sfa = O.quant_act_nvfp4(xa, 0.0125)
+    qs, sfs = O.silu_mul_quant_nvfp4(xa, xu, 0.0125)
+    v["act_nvfp4"] = {"x": hexa(xa), "u": hexa(xu), "input_scale": 0.0125, "q": hexa(qa), "sf": hexa(sfa),
+                      "silu_q": hexa(qs), "silu_sf": hexa(sfs)}
+    xr = O.normal_f32(0x4C51F008, 1.0, (2, 1024))
+    wr = O.normal_bf16(0x4C51F009, 0.1, 1024)
+    o8, q8, _ = O.rmsnorm_quant(xr, wr, 1e-6, False, 0.02)
+    o4, q4, sf4 = O.rmsnorm_quant(xr, wr, 1e-6, True, 0.005)
+    v["rmsnorm_quant"] = {"x": hexa(xr), "w_bf16": hexa(wr), "eps": 1e-6, "out": hexa(o8), "fp8_input_scale": 0.02,
+                          "fp8_q": hexa(q8), "nvfp4_input_scale": 0.005, "nvfp4_q": hexa(q4), "nvfp4_sf": hexa(sf4)}
+    assert np.array_equal(o4, o8)
+    # NVFP4 prefill rows (float64 over exactly dequantized operands), M=2, N=16, K=128
+    qx, sfx = O.quant_act_nvfp4(O.normal_f32(0x4C51F00A, 1.0, (2, 128)), 0.0125)
+    v["prefill_nvfp4"] = {"xq": hexa(qx), "xs": hexa(sfx), "alpha": 0.0125 * float(g),
+                          "y_f64": hexa(O.prefill_nvfp4_rows(qx, sfx, np.arange(2), vals, sc, 0.0125 * float(g)))}
     return v
 
 
