@@ -1,6 +1,6 @@
 """Benchmark of the fused quantized GEMM path on one MI355X.
 
-Headline (BASELINE.json metric): the speculative-verify MLP at M = 17 rows (config 2): gate|up
+Headline metric: the speculative-verify MLP at M = 17 rows (config 2): gate|up
 (K = 5120, N = 2 x 17408, FP8 per-channel) with the SiLU*mul epilogue, then down (K = 17408, N = 5120) with the
 BF16 residual add. A step is one such pass (two launches); `value` is algorithmic HBM bytes per second of the whole
 step (the same pass as the one-launch FFN kernel is reported beside it).
@@ -322,7 +322,7 @@ def bench_prefill(torch, L, O, args, dev):
 
 def bench_prefill_nvfp4(torch, L, args, dev):
     """The NVFP4 prefill GEMM on config 4's gate|up shape (M = 4096, N = 2 x 17408, K = 5120) and the fused SwiGLU
-    form (gate and up, N = 17408 each, into NVFP4): a beside-line, not a BASELINE config (its prefill is FP8)."""
+    form (gate and up, N = 17408 each, into NVFP4): a beside-line, not one of the benchmark configs (their prefill is FP8)."""
     M, H, F = 4096, 5120, 17408
     g = torch.Generator(device=dev)
     g.manual_seed(11)
@@ -467,7 +467,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) BF16 activations; random FP8 E4M3 weight codes, per-channel scales)",
         "config": {"workload": "speculative-verify MLP, M=17: gate|up 5120->2x17408 FP8 per-channel + SiLU*mul, "
-                               "down 17408->5120 + BF16 residual (BASELINE config 2)",
+                               "down 17408->5120 + BF16 residual (benchmark config 2)",
                    "M": 17, "hidden": 5120, "ffn": 17408, "weight_format": "fp8_e4m3 per-channel",
                    "rotation_copies": vm["rotation_copies"]},
         "frac_hbm": round(vm["gb_s"] / HBM_PEAK_GBS, 4),

@@ -102,7 +102,7 @@ def test_prefill_stray_columns_and_rows(L):
 
 @pytest.mark.parametrize("N,K", [(34816, 5120), (5120, 17408)])
 def test_prefill_config4_shapes_row_subset(L, N, K):
-    """BASELINE config 4 (M = 4096): the full GEMM on the GPU, checked on every 64th token row."""
+    """The prefill benchmark shape (M = 4096, config 4): the full GEMM on the GPU, checked on every 64th token row."""
     M = 4096
     rng = np.random.default_rng(N)
     wq = rng.integers(0, 256, (N, K), dtype=np.uint8)

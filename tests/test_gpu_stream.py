@@ -1,6 +1,6 @@
 """Parity of the skinny (stream) GEMMs on the GPU against the CPU oracle, through the C ABI.
 
-Bounds: on BF16 outputs, max relative error <= 1e-2 and mean |got - ref| <= 1e-3, with the
+Bounds (the path's accuracy target): on BF16 outputs, max relative error <= 1e-2 and mean |got - ref| <= 1e-3, with the
 relative error of an element |got - ref| / max(|ref|, rms(ref row)) (robust to outputs near zero; one BF16 ulp is
 at most 2^-8 of it),
 where ref is the oracle (dequantize to FP32, FP32 accumulate, one BF16 rounding); dequantized weights and the
