@@ -49,19 +49,21 @@ constexpr int kMaxMats = 4;
 
 enum WFmt { kFp8 = 0, kFp4 = 1, kFp4Coded = 2 };
 
-// 16-row tiles per wave: one gate and one up tile with the SiLU*mul epilogue; two FP8 tiles; four NVFP4 tiles
+// 16-row tiles per wave (T): one gate and one up tile with the SiLU*mul epilogue; two FP8 tiles; four NVFP4 tiles
 // (half the bytes per tile and chunk). Enough weight bytes per load stage keep the HBM stream deep, and every
-// activation operand read from LDS feeds T MFMAs. Fixed per format (never chosen by M: row invariance).
+// activation operand read from LDS feeds T MFMAs. One FP8 tile per wave instead where each workgroup's range is
+// short (choose_tiles): there the split-K finish, whose fan-in halves with T, outweighs the stream's depth.
+// Chosen by N, K and the CU count only, never by M (row invariance).
 __host__ __device__ constexpr int tiles_per_wave(int wf, bool pair) { return pair ? 2 : wf == kFp8 ? 2 : 4; }
 // Output rows (columns of y) per tile group: the workgroup's 4 waves' tiles (gate rows only for a pair).
-__host__ __device__ constexpr int group_rows(int wf, bool pair) {
-  return 16 * 4 * (pair ? tiles_per_wave(wf, pair) / 2 : tiles_per_wave(wf, pair));
-}
+__host__ __device__ constexpr int group_rows(int T, bool pair) { return 16 * 4 * (pair ? T / 2 : T); }
 
 // Weight chunks in flight per wave (the computed one included), by register budget.
 template <int T>
 __host__ __device__ constexpr int pf_stages(int G) {
-  return T == 2 ? (G <= 1 ? 8 : G <= 2 ? 6 : 4) : (G <= 1 ? 6 : G <= 2 ? 4 : G <= 3 ? 3 : 2);
+  return T == 1   ? (G <= 1 ? 12 : G <= 2 ? 10 : G <= 3 ? 8 : 6)
+         : T == 2 ? (G <= 1 ? 8 : G <= 2 ? 6 : 4)
+                  : (G <= 1 ? 6 : G <= 2 ? 4 : G <= 3 ? 3 : 2);
 }
 
 struct StreamArgs {
@@ -71,6 +73,7 @@ struct StreamArgs {
   int P;              // logical workgroups
   int U;              // units = TG * C (U * (P + 1) < 2^31: the unit arithmetic is 32-bit)
   int TG;             // tile groups
+  int T;              // tiles per wave (the kernel's template argument)
   int count;          // matrices
   const uint8_t* w[kMaxMats];
   const uint8_t* table[kMaxMats];   // coded NVFP4: device scale-code table [64]
@@ -328,7 +331,7 @@ __device__ __forceinline__ void seg_tiles(const StreamArgs& a, int tg, int wave,
     while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
   }
   s.mi = mi;
-  s.wtile0 = (tg - a.tg0[mi]) * (group_rows(WF, PAIR) / 16) + wave * (PAIR ? T / 2 : T);
+  s.wtile0 = (tg - a.tg0[mi]) * (group_rows(T, PAIR) / 16) + wave * (PAIR ? T / 2 : T);
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
@@ -497,9 +500,9 @@ __device__ __forceinline__ int logical_wg(int P) {
   return p;
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32, int MODE, class Ready>
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, int MODE, class Ready>
 __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>& sm, Ready&& ready) {
-  constexpr int T = tiles_per_wave(WF, PAIR);
+  constexpr int T = TW;
   constexpr int PF = pf_stages<T>(G);
   constexpr bool BPRE = Smem<G>::BPRE;
   constexpr int NSLOT = Smem<G>::NSLOT;
@@ -853,10 +856,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   flush_trace(p);
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
-  stream_body<G, WF, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg(a.P), sm, NoWait{});
+  stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg(a.P), sm, NoWait{});
 }
 
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
@@ -873,7 +876,7 @@ template <int G>
 __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const StreamArgs b, int* sync) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
   const int p = logical_wg(a.P);
-  stream_body<G, kFp8, false, true, false, kYCoh>(a, p, sm, NoWait{});
+  stream_body<G, kFp8, 2, false, true, false, kYCoh>(a, p, sm, NoWait{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores have completed
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -891,7 +894,7 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
     }
     __syncthreads();
   };
-  stream_body<G, kFp8, false, false, false, kXCoh>(b, p, sm, ready);
+  stream_body<G, kFp8, 2, false, false, false, kXCoh>(b, p, sm, ready);
   __syncthreads();
   if (threadIdx.x == 0 &&
       __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1) {
@@ -1132,21 +1135,30 @@ int choose_wgs(long long U) {
   return static_cast<int>(std::max<long long>(P, 1));
 }
 
-template <int G, int WF, bool F16, bool PAIR, bool OUTF32, bool CVT>
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g(const StreamArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((stream_kernel<G, WF, F16, PAIR, OUTF32, CVT>), dim3(a.P), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), dim3(a.P), dim3(kThreads), 0, s, a);
   return check_launch("stream_gemm");
 }
 
+template <int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
+int launch_mt(const StreamArgs& a, hipStream_t s) {
+  switch (cdiv(a.M, 16)) {
+    case 1: return launch_g<1, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+    case 2: return launch_g<2, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+    case 3: return launch_g<3, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+    case 4: return launch_g<4, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+    default: return launch_g<5, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+  }
+}
+
+// Dispatch on the tiles per wave stream_args chose (only FP8 single matrices have a choice).
 template <int WF, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 int launch_m(const StreamArgs& a, hipStream_t s) {
-  switch (cdiv(a.M, 16)) {
-    case 1: return launch_g<1, WF, F16, PAIR, OUTF32, CVT>(a, s);
-    case 2: return launch_g<2, WF, F16, PAIR, OUTF32, CVT>(a, s);
-    case 3: return launch_g<3, WF, F16, PAIR, OUTF32, CVT>(a, s);
-    case 4: return launch_g<4, WF, F16, PAIR, OUTF32, CVT>(a, s);
-    default: return launch_g<5, WF, F16, PAIR, OUTF32, CVT>(a, s);
+  if constexpr (WF == kFp8 && !PAIR) {
+    if (a.T == 1) return launch_mt<WF, 1, F16, PAIR, OUTF32, CVT>(a, s);
   }
+  return launch_mt<WF, tiles_per_wave(WF, PAIR), F16, PAIR, OUTF32, CVT>(a, s);
 }
 
 // Validates, fills the launch arguments and launches. `fmt`: weight format; `f16`: activations are an
@@ -1156,8 +1168,35 @@ unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the
 #endif
 
 // FP32 floats of one partial slot (one workgroup's T x G accumulator vectors for 256 threads).
-size_t slot_floats(int fmt, bool pair, int M) {
-  return static_cast<size_t>(tiles_per_wave(fmt, pair)) * cdiv(M, 16) * 4 * kThreads;
+size_t slot_floats(int T, int M) { return static_cast<size_t>(T) * cdiv(M, 16) * 4 * kThreads; }
+
+// Tiles per wave and the split for these matrices (sets a.T, a.TG, a.P, a.U). One FP8 tile per wave when a
+// workgroup's range would be short (under 10 chunks at two tiles) and a tile group would span more than 4
+// workgroups: there the finish dominates, and one tile per wave halves its fan-in and partial size. Depends on
+// the matrices' N, K and the device only, never on M (row invariance).
+int choose_tiles(const char* name, int fmt, bool pair, const int* Ns, int n, StreamArgs& a) {
+  auto split = [&](int T, long long& tg, long long& units, int& P) {
+    tg = 0;
+    if (pair) tg = cdiv(Ns[0], group_rows(T, true));
+    else
+      for (int i = 0; i < n; ++i) tg += cdiv(Ns[i], group_rows(T, false));
+    units = tg * a.C;
+    P = choose_wgs(units);
+  };
+  int T = tiles_per_wave(fmt, pair);
+  long long tg, units;
+  int P;
+  split(T, tg, units, P);
+  if (fmt == kFp8 && !pair && units < 10LL * P && P > 4 * tg) {
+    T = 1;
+    split(T, tg, units, P);
+  }
+  if (units * (P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, std::string(name) + ": matrices too large for one launch");
+  a.T = T;
+  a.TG = static_cast<int>(tg);
+  a.P = P;
+  a.U = static_cast<int>(units);
+  return LQ_OK;
 }
 
 // Validates and fills the launch arguments except the workspace pointers.
@@ -1176,7 +1215,7 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
   a.K = K;
   a.C = K / kChunk;
   a.count = n;
-  int tg = 0;
+  int Ns[kMaxMats];
   for (int i = 0; i < n; ++i) {
     const Mat& m = mats[i];
     if (m.N <= 0 || m.N % 16 != 0) return fail(LQ_ERR_SHAPE, nm + ": N % 16 and K % 128 must be 0");
@@ -1194,19 +1233,16 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
     a.resid[i] = m.resid;
     a.N[i] = m.N;
     a.ldy[i] = m.ldy;
+    Ns[i] = m.N;
+  }
+  if (pair && (n != 2 || mats[0].N != mats[1].N)) return fail(LQ_ERR_SHAPE, nm + ": gate and up must have the same N");
+  if (int rc = choose_tiles(name, fmt, pair, Ns, n, a)) return rc;
+  int tg = 0;
+  for (int i = 0; i < n; ++i) {
     a.tg0[i] = tg;
-    if (!pair) tg += cdiv(m.N, group_rows(fmt, false));
+    if (!pair) tg += cdiv(Ns[i], group_rows(a.T, false));
   }
-  if (pair) {
-    if (n != 2 || mats[0].N != mats[1].N) return fail(LQ_ERR_SHAPE, nm + ": gate and up must have the same N");
-    tg = cdiv(mats[0].N, group_rows(fmt, true));
-  }
-  a.tg0[n] = tg;
-  a.TG = tg;
-  const long long units = static_cast<long long>(tg) * a.C;
-  a.P = choose_wgs(units);
-  if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrices too large for one launch");
-  a.U = static_cast<int>(units);
+  a.tg0[n] = a.TG;
   if (!pair && fmt != kFp8 && !f16 && outf32) return fail(LQ_ERR_ARG, nm + ": BF16 activations with NVFP4 give BF16 out");
   return LQ_OK;
 }
@@ -1218,7 +1254,7 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   if (rc) return rc;
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  rc = ws->reserve_stream(2 * static_cast<size_t>(a.P) * slot_floats(fmt, pair, M) * sizeof(float),
+  rc = ws->reserve_stream(2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float),
                           static_cast<size_t>(a.TG));
   if (rc) return rc;
   a.partials = ws->partials;
@@ -1247,14 +1283,14 @@ int ffn_launch(const char* name, const uint16_t* x, int M, const Mat (&gu)[2], c
   if (rc) return rc;
   rc = stream_args(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, b);
   if (rc) return rc;
-  if (a.P != b.P) {
+  if (a.P != b.P || b.T != 2) {  // (the one-launch form runs its down phase at two tiles per wave)
     rc = stream_launch(name, kFp8, false, true, false, x, nullptr, M, gu, 2, dn.N, s);
     return rc ? rc : stream_launch(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, s);
   }
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  const size_t fa = 2 * static_cast<size_t>(a.P) * slot_floats(kFp8, true, M);
-  const size_t fb = 2 * static_cast<size_t>(b.P) * slot_floats(kFp8, false, M);
+  const size_t fa = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M);
+  const size_t fb = 2 * static_cast<size_t>(b.P) * slot_floats(b.T, M);
   rc = ws->reserve_stream((fa + fb) * sizeof(float), static_cast<size_t>(a.TG) + b.TG);
   if (rc) return rc;
   a.partials = ws->partials;
@@ -1425,8 +1461,9 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.cap = cap;
   a.N = N;
   a.y = y;
-  // the full launch's split (stream_launch for this N, K): tile groups of group_rows(kFp4) rows
-  a.TGR = group_rows(kFp4, false);
+  // the full launch's split (stream_launch for this N, K): tile groups of group_rows(4) rows (NVFP4 always runs
+  // four tiles per wave)
+  a.TGR = group_rows(tiles_per_wave(kFp4, false), false);
   const long long units = static_cast<long long>(cdiv(N, a.TGR)) * a.C;
   a.P = choose_wgs(units);
   if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrix too large");
