@@ -385,3 +385,17 @@ def test_caller_workspace(L):
         L.set_workspace(None)
     torch.cuda.synchronize()
     assert all(torch.equal(a, b) for a, b in zip(own, run()))
+
+
+@pytest.mark.parametrize("N,K", [(5120, 5120), (5120, 6144), (7168, 5120)])
+def test_full_size_one_tile_shapes(L, N, K):
+    """Config 1's decode GEMV (M = 1, 5120 x 5120) and the short-range shapes of the decode step that run one tile
+    per wave: parity at M = 1 and M = 17 against the oracle, and rows of M = 1 and 17 bit-identical to M = 68."""
+    q, s = fp8_weights(91, N, K)
+    x = O.normal_bf16(92, 1.0, (68, K))
+    tw, sd, xd = L.retile_fp8(to_dev(q)), to_dev(s), bf16_dev(x)
+    full = bf16_host(L.stream_fp8_pc(xd, tw, sd, N))
+    for M in (1, 17):
+        got = bf16_host(L.stream_fp8_pc(xd[:M].contiguous(), tw, sd, N))
+        assert_close_bf16(got, O.stream_fp8_pc_bf16(x[:M], q, s), f"M={M} N={N} K={K}")
+        assert np.array_equal(got, full[:M]), f"row invariance M={M} N={N} K={K}"
