@@ -397,6 +397,77 @@ def cpu_baseline(O):
                       f"{best * threads:.1f} core-seconds"}
 
 
+def bench_producers(torch, L, args, dev):
+    """The activation producers at config 4's shapes (M = 4096 tokens) and the sparse-head gather (M = 17, 2048
+    of 151936 vocabulary rows of a 5120-wide NVFP4 head): all HBM-bound, so each reports its bytes moved (inputs
+    read once, outputs written once), the time per launch (HIP events over back-to-back launches rotating over
+    input copies of >= 1 GB) and the fraction of 8 TB/s."""
+    M, H, F = 4096, 5120, 17408
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x4C51000A)
+
+    def timed(fn, copies, reps=40):
+        for i in range(3):
+            fn(i % copies)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(reps):
+            fn(i % copies)
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / reps
+
+    def line(name, nbytes, ms):
+        return {"bytes": nbytes, "us": round(ms * 1e3, 2), "gb_s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(nbytes / (ms * 1e-3) / 8e12, 4)}
+
+    out = {}
+    nb = M * H
+    # 1x128 FP8 group quantizer: BF16 in, FP8 + FP32 group scales out
+    c = max(2, -(-(1 << 30) // (2 * nb)))
+    xs = [torch.randn(M, H, device=dev, generator=g).to(torch.bfloat16) for _ in range(c)]
+    byt = 2 * nb + nb + nb // 128 * 4
+    out["quant_act_fp8_g128"] = line("g128", byt, timed(lambda i: L.quant_act_fp8_g128(xs[i]), c))
+    del xs
+    # NVFP4 quantizer and RMSNorm into NVFP4 (no FP32 copy): FP32 in, packed E2M1 + E4M3 block scales out
+    c = max(2, -(-(1 << 30) // (4 * nb)))
+    xf = [torch.randn(M, H, device=dev, generator=g) for _ in range(c)]
+    byt = 4 * nb + nb // 2 + nb // 16
+    out["quant_act_nvfp4"] = line("nvfp4", byt, timed(lambda i: L.quant_act_nvfp4(xf[i], 0.01), c))
+    w = (torch.randn(H, device=dev, generator=g) * 0.1).to(torch.bfloat16).view(torch.int16)
+    out["rmsnorm_quant_nvfp4"] = line("rmsq", byt + 2 * H, timed(
+        lambda i: L.rmsnorm_quant(xf[i], w, 1e-6, True, 0.01, with_out=False), c))
+    del xf
+    # silu(g) * u into NVFP4 (the FFN's gate|up outputs, FP32): two inputs
+    nf = M * F
+    c = 2
+    gu = [(torch.randn(M, F, device=dev, generator=g), torch.randn(M, F, device=dev, generator=g)) for _ in range(c)]
+    byt = 8 * nf + nf // 2 + nf // 16
+    out["silu_mul_quant_nvfp4"] = line("silu", byt, timed(lambda i: L.silu_mul_quant_nvfp4(gu[i][0], gu[i][1], 0.01), c))
+    del gu
+    torch.cuda.empty_cache()
+    # sparse-head gather: 2048 of 151936 rows of an NVFP4 [151936][5120] head, M = 17 (a verify step's rows)
+    V, K, Mg, cap = 151936, 5120, 17, 2048
+    vals = torch.randint(0, 256, (V, K // 2), dtype=torch.uint8, device=dev, generator=g)
+    scs = torch.randint(0x28, 0x48, (V, K // 16), dtype=torch.uint8, device=dev, generator=g)
+    head = L.retile_nvfp4(vals, scs)
+    del vals, scs
+    xh, xinv = L.bf16_to_half_rows(torch.randn(Mg, K, device=dev, generator=g).to(torch.bfloat16))
+    sets = []
+    for c2 in range(8):
+        rows = torch.randperm(V, device=dev, generator=g)[:cap].to(torch.int32)
+        sets.append(rows)
+    nrows = torch.tensor([cap], dtype=torch.int32, device=dev)
+    y = torch.empty((Mg, cap), dtype=torch.float32, device=dev)
+    byt = cap * (K // 2 + K // 16) + Mg * K * 2 + Mg * cap * 4
+    out["gather_nvfp4_2048_of_151936"] = line("gather", byt, timed(
+        lambda i: L.stream_gemm_gather_nvfp4(xh, xinv, head, None, 1e-3, sets[i], nrows, cap, V, K, y=y), 8))
+    del head
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -434,6 +505,10 @@ def main():
         pn = bench_prefill_nvfp4(torch, L, args, dev)
         extra["prefill_nvfp4_m4096"] = pn
         log(f"[bench] prefill nvfp4: {pn}")
+    if only is None or "producers" in only:
+        pr = bench_producers(torch, L, args, dev)
+        extra["producers"] = pr
+        log(f"[bench] producers: {pr}")
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

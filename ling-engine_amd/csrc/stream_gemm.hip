@@ -39,6 +39,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <utility>
 
 namespace lq {
 namespace {
@@ -911,6 +912,17 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
 // stream-K split cuts that row's tile group (workgroup boundaries of the full launch's P and units), and the
 // segments added left to right as its finisher adds them. A wave computes 16 gathered rows; a lane's four
 // output rows may belong to different tile groups, so each keeps its own next cut.
+// Calls f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>) in order: a body unrolled at compile time,
+// so register arrays indexed by the constant stay in registers.
+template <class F, int... J>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 struct GatherArgs {
   const void* x;      // FP16 [M][K]
   const float* xinv;  // [M]
@@ -925,14 +937,22 @@ struct GatherArgs {
   float* y;          // [M][cap]
 };
 
+// One wave per workgroup and no LDS: a lane's B operand for a chunk is 64 contiguous bytes of one activation row
+// (row 16g + r, halves 32t .. 32t + 31 of the chunk, the four MFMA steps' 16-byte pieces in order), loaded from
+// L2 straight into registers. Loads run D chunks ahead of the MFMA steps, so a wave's serial path per chunk is
+// its MFMA chain alone, and the waves never wait on each other.
+constexpr int kGatherThreads = 64;
 template <int G>
-__global__ void __launch_bounds__(kThreads) gather_kernel(const GatherArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t xs[16 * G * 256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+struct GatherDepth {
+  static constexpr int D = G == 1 ? 8 : G == 2 ? 4 : 2;  // chunks in flight: 16 * G * D activation VGPRs
+};
+
+template <int G>
+__global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs a) {
+  const int lane = threadIdx.x & 63;
   const int r = lane & 15, t = lane >> 4;
   const int cnt = min(max(*a.nrows, 0), a.cap);
-  const int i0 = (blockIdx.x * kWaves + wave) * 16;  // this wave's first gathered row
-  const bool any = static_cast<int>(blockIdx.x) * kWaves * 16 < cnt;  // uniform over the workgroup
+  const int i0 = static_cast<int>(blockIdx.x) * 16;  // this wave's first gathered row
   // epilogue rows of this lane: gathered i = i0 + 4t + v, token 16g + r
   auto store = [&](const float (&val)[G][4]) {
 #pragma unroll
@@ -946,7 +966,7 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const GatherArgs a) {
       }
     }
   };
-  if (!any) {
+  if (i0 >= cnt) {  // uniform over the wave
     float ninf[G][4];
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -977,14 +997,13 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const GatherArgs a) {
     nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
     first[v] = true;
   }
-  // activations: thread's share of a chunk as in the stream kernel
+  // the lane's activation bytes: row 16g + r from byte 64t of each chunk (rows >= M read as zeros)
   const __amdgpu_buffer_rsrc_t xrs = make_rsrc(a.x);
-  int xsrc[G], xdst[G];
+  unsigned xoff[G];
 #pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const int q = i * kThreads + static_cast<int>(threadIdx.x), row = q >> 4, u = q & 15;
-    xsrc[i] = row < a.M ? (row * a.K) * 2 + u * 16 : static_cast<int>(0x80000000u);
-    xdst[i] = xs_off(row, u);
+  for (int g = 0; g < G; ++g) {
+    const int m = 16 * g + r;
+    xoff[g] = m < a.M ? static_cast<unsigned>(m * a.K * 2 + t * 64) : 0x80000000u;
   }
   f32x4 acc[1][G];
   float tot[G][4];
@@ -995,40 +1014,65 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const GatherArgs a) {
     for (int v = 0; v < 4; ++v) tot[g][v] = 0.f;
   }
   const uint8_t* const tab[1] = {nullptr};
-  for (int c = 0; c < a.C; ++c) {
-#pragma unroll
-    for (int i = 0; i < G; ++i)
-      *reinterpret_cast<u32x4*>(xs + xdst[i]) = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xsrc[i]), c * 256, 0));
-    WRegs<kFp4, 1> R;
-    const size_t blk = static_cast<size_t>(nac >> 4) * a.C + c;
-    R.v[0][0] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>((blk * blk_bytes + slot * 16) | aoob), 0, 0));
+  constexpr int D = GatherDepth<G>::D;
+  u32x4 xr[D][G][4], wv[D];
+  uint32_t wsc[D];
+  const size_t row_blk = static_cast<size_t>(nac >> 4) * a.C;
+  auto issue = [&](auto J, int cc) {
+    constexpr int j = decltype(J)::value;
+    const unsigned o = cc < a.C ? 0u : 0x80000000u;  // past the last chunk: out of range, reads as zeros
+    const int cl = min(cc, a.C - 1);
+    const size_t blk = row_blk + cl;
+    wv[j] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, static_cast<int>((blk * blk_bytes + slot * 16) | aoob | o), 0, 0));
     const size_t so = a.raw ? blk * 128 + slot * 2 : blk * kTileBytesFp4 + 1024 + slot * 2;
-    R.sc[0] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, static_cast<int>(so | aoob), 0, 0));
-    __syncthreads();
-    u32x4 b[G];
+    wsc[j] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, static_cast<int>(so | aoob | o), 0, 0));
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      read_b<G>(b, xs, s, r, t);
-      mfma_step<kFp4, true, G, 1>(R, s, b, acc, tab);
-    }
-    __syncthreads();
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      if (c == nb[v]) {
+      for (int s = 0; s < 4; ++s)
+        xr[j][g][s] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xoff[g] | o), cl * 256 + s * 16, 0));
+  };
+  static_for<D>([&](auto J) { issue(J, J); });
+  for (int c0 = 0; c0 < a.C; c0 += D) {
+    static_for<D>([&](auto J) {
+      constexpr int j = decltype(J)::value;
+      // a chunk past the last one (C % D != 0) reads zeros and adds +0 to an accumulator no cut reads: no branch,
+      // so the ring's loads stay in flight across the chunk
+      const int c = c0 + j;
+      WRegs<kFp4, 1> R;
+      R.v[0][0] = wv[j];
+      R.sc[0] = wsc[j];
+      u32x4 xb[G][4];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-          tot[g][v] = first[v] ? acc[0][g][v] : tot[g][v] + acc[0][g][v];
-          acc[0][g][v] = 0.f;
-        }
-        first[v] = false;
-        if (c + 1 < a.C) {
-          const int p = wg_of_unit(tgc[v] + c + 1, a.P, a.U);
-          nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) xb[g][s] = xr[j][g][s];
+      issue(J, c + D);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        u32x4 b[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) b[g] = xb[g][s];
+        mfma_step<kFp4, true, G, 1>(R, s, b, acc, tab);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if (c == nb[v]) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            tot[g][v] = first[v] ? acc[0][g][v] : tot[g][v] + acc[0][g][v];
+            acc[0][g][v] = 0.f;
+          }
+          first[v] = false;
+          if (c + 1 < a.C) {
+            const int p = wg_of_unit(tgc[v] + c + 1, a.P, a.U);
+            nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+          }
         }
       }
-    }
+    });
   }
   float val[G][4];
 #pragma unroll
@@ -1468,14 +1512,14 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.P = choose_wgs(units);
   if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrix too large");
   a.U = static_cast<int>(units);
-  const dim3 grid(cdiv(cap / 16, kWaves));
+  const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cdiv(M, 16)) {
-    case 1: hipLaunchKernelGGL(gather_kernel<1>, grid, dim3(kThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(gather_kernel<2>, grid, dim3(kThreads), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(gather_kernel<3>, grid, dim3(kThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(gather_kernel<4>, grid, dim3(kThreads), 0, s, a); break;
-    default: hipLaunchKernelGGL(gather_kernel<5>, grid, dim3(kThreads), 0, s, a); break;
+    case 1: hipLaunchKernelGGL(gather_kernel<1>, grid, blk, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(gather_kernel<2>, grid, blk, 0, s, a); break;
+    case 3: hipLaunchKernelGGL(gather_kernel<3>, grid, blk, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(gather_kernel<4>, grid, blk, 0, s, a); break;
+    default: hipLaunchKernelGGL(gather_kernel<5>, grid, blk, 0, s, a); break;
   }
   return check_launch("stream_gemm_gather");
 }
