@@ -178,13 +178,15 @@ int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float 
                             void* stream);
 /* Gemma RMSNorm of each row, v = x * rstd * (1 + w) with rstd = 1 / sqrt(mean(x^2) + eps), into `out` (FP32,
  * may be null) and straight into the next GEMM's encoding: NVFP4 (q [M][H/2], sf [M][H/16]) when nvfp4, else FP8
- * E4M3(BF16(v) / input_scale) saturated (q [M][H]). H % 1024 == 0. kernels.cuh:203-204 rmsnorm_quant. */
+ * E4M3(BF16(v) / input_scale) saturated (q [M][H]). H % 1024 == 0, H <= 65536; x, w, out, q 16-byte aligned.
+ * kernels.cuh:203-204 rmsnorm_quant. */
 int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
                      float input_scale, uint8_t* q, uint8_t* sf, void* stream);
 
 /* ---------------- prefill, block-scaled FP8 (additive; reference src/core/kernels.cuh:190-221) ---------------- */
 /* BF16 x [M][K] -> FP8 E4M3 q [M][K] with one FP32 scale per 1x128 group, scale [M][K/128] = amax / 448 (1 for an
- * all-zero group), q = E4M3_rne(x / scale). The block-scaled counterpart of quant_act_fp8 (kernels.cuh:199). */
+ * all-zero group), q = E4M3_rne(x / scale); x 16-byte and q 8-byte aligned. The block-scaled counterpart of
+ * quant_act_fp8 (kernels.cuh:199). */
 int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* scale, void* stream);
 /* y[M][0..N) (rows ldy apart, BF16) = bf16(sum over 128-value K blocks kb of (xq . W^T over kb) * xs[m][kb] *
  * ws[n/128][kb]); xq FP8 [M][K], xs FP32 [M][K/128], W tiled FP8 (the stream GEMMs' blob), ws FP32 [N/128][K/128].

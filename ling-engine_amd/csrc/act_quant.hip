@@ -70,45 +70,61 @@ __global__ void __launch_bounds__(256) quant_nvfp4_kernel(const float* __restric
   }
 }
 
-// One workgroup per row: the sum of squares (each thread's float4 slices, then the wave and the four waves
-// in a fixed order), rstd = 1 / sqrt(sum / H + eps), v = x * rstd * (1 + w) (written to `out` when given),
-// then each thread quantizes whole 16-value blocks of BF16(v): NVFP4, or FP8 E4M3(BF16(v) / input_scale).
-template <bool FP4>
-__global__ void __launch_bounds__(256) rmsnorm_quant_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
-                                                            float* __restrict__ out, int H, float eps, float g,
-                                                            uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
-  __shared__ float red[4];
+// One workgroup per row, one thread per 16-value block (NB <= 4 blocks per thread when the row has more than 1024,
+// so H <= 65536), the row held in registers from a single read: the sum of squares (each thread's values in
+// order, then the wave, then the waves in order), rstd = 1 / sqrt(sum / H + eps), v = x * rstd * (1 + w)
+// (written to `out` when given), then the thread quantizes its blocks of BF16(v): NVFP4, or FP8
+// E4M3(BF16(v) / input_scale).
+template <bool FP4, int NB>
+__global__ void __launch_bounds__(1024) rmsnorm_quant_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
+                                                             float* __restrict__ out, int H, float eps, float g,
+                                                             uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
+  __shared__ float red[16];
   const size_t r = blockIdx.x;
+  const int nblk = H / 16, T = static_cast<int>(blockDim.x);
   const float* row = x + r * H;
+  f32x4 f[NB][4];
   float ss = 0.f;
-  for (int i = threadIdx.x; i < H / 4; i += 256) {
-    const f32x4 f = reinterpret_cast<const f32x4*>(row)[i];
-    ss = __builtin_fmaf(f[0], f[0], ss);
-    ss = __builtin_fmaf(f[1], f[1], ss);
-    ss = __builtin_fmaf(f[2], f[2], ss);
-    ss = __builtin_fmaf(f[3], f[3], ss);
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int blk = static_cast<int>(threadIdx.x) + j * T;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      f[j][k] = blk < nblk ? reinterpret_cast<const f32x4*>(row)[blk * 4 + k] : f32x4{0.f, 0.f, 0.f, 0.f};
   }
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(f[j][k][e], f[j][k][e], ss);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
   __syncthreads();
-  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float tot = 0.f;
+  for (int i = 0; i < T / 64; ++i) tot += red[i];
   const float rstd = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
-  for (int blk = threadIdx.x; blk < H / 16; blk += 256) {
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int blk = static_cast<int>(threadIdx.x) + j * T;
+    if (blk >= nblk) continue;
+    const u32x4 w0 = reinterpret_cast<const u32x4*>(w)[blk * 2], w1 = reinterpret_cast<const u32x4*>(w)[blk * 2 + 1];
+    const uint32_t wp[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
     float v[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const f32x4 f = reinterpret_cast<const f32x4*>(row)[blk * 4 + k];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int h = blk * 16 + 4 * k + e;
-        v[4 * k + e] = f[e] * rstd * (1.f + bf16_to_f32(w[h]));
+        const int h = 4 * k + e;
+        const uint32_t wb = (h & 1) ? wp[h >> 1] >> 16 : wp[h >> 1] & 0xffff;
+        v[h] = f[j][k][e] * rstd * (1.f + bf16_to_f32(wb));
       }
       if (out) reinterpret_cast<f32x4*>(out + r * H)[blk * 4 + k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = bf16_round(v[i]);
-    const size_t b = r * (H / 16) + blk;
+    const size_t b = r * nblk + blk;
     if constexpr (FP4) {
       put_nvfp4_block(v, g, q + b * 8, sf + b);
     } else {
@@ -122,6 +138,17 @@ __global__ void __launch_bounds__(256) rmsnorm_quant_kernel(const float* __restr
       reinterpret_cast<u32x4*>(q)[b] = u32x4{wq[0], wq[1], wq[2], wq[3]};
     }
   }
+}
+
+template <bool FP4>
+void rmsnorm_launch(int M, int H, hipStream_t s, const float* x, const uint16_t* w, float* out, float eps, float g,
+                    uint8_t* q, uint8_t* sf) {
+  const int nblk = H / 16;
+  const int T = nblk < 1024 ? nblk : 1024;  // H % 1024 == 0: a multiple of 64
+  const int nb = (nblk + T - 1) / T;
+  if (nb == 1) hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 1>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+  else if (nb == 2) hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 2>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+  else hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 4>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
 }
 
 unsigned grid_for(size_t items) {
@@ -139,6 +166,8 @@ extern "C" {
 int lq_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
   if (M < 1 || K <= 0 || K % 16 != 0) return fail(LQ_ERR_SHAPE, "quant_act_nvfp4: M >= 1 and K % 16 == 0");
   if (!x || !q || !sf) return fail(LQ_ERR_ARG, "quant_act_nvfp4: null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q) % 8 != 0)
+    return fail(LQ_ERR_ARG, "quant_act_nvfp4: x must be 16-byte and q 8-byte aligned");
   const size_t blocks = static_cast<size_t>(M) * K / 16;
   hipLaunchKernelGGL(quant_nvfp4_kernel<false>, dim3(grid_for(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), x,
                      nullptr, blocks, 1.f / input_scale, q, sf);
@@ -149,6 +178,8 @@ int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float 
                             void* stream) {
   if (M < 1 || K <= 0 || K % 16 != 0) return fail(LQ_ERR_SHAPE, "silu_mul_quant_nvfp4: M >= 1 and K % 16 == 0");
   if (!g || !u || !q || !sf) return fail(LQ_ERR_ARG, "silu_mul_quant_nvfp4: null pointer");
+  if ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u)) % 16 != 0 || reinterpret_cast<uintptr_t>(q) % 8 != 0)
+    return fail(LQ_ERR_ARG, "silu_mul_quant_nvfp4: g and u must be 16-byte and q 8-byte aligned");
   const size_t blocks = static_cast<size_t>(M) * K / 16;
   hipLaunchKernelGGL(quant_nvfp4_kernel<true>, dim3(grid_for(blocks)), dim3(256), 0, static_cast<hipStream_t>(stream), g,
                      u, blocks, 1.f / input_scale, q, sf);
@@ -159,13 +190,14 @@ int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H
                      float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
   if (M < 1) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: M must be positive");
   if (H <= 0 || H % 1024 != 0) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: H % 1024 must be 0");
+  if (H > 65536) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: H must be at most 65536 (the row is held in registers)");
   if (!x || !w || !q || (nvfp4 && !sf)) return fail(LQ_ERR_ARG, "rmsnorm_quant: null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(q)) % 16 != 0)
+    return fail(LQ_ERR_ARG, "rmsnorm_quant: x, w, out and q must be 16-byte aligned");
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (nvfp4)
-    hipLaunchKernelGGL(rmsnorm_quant_kernel<true>, dim3(M), dim3(256), 0, s, x, w, out, H, eps, 1.f / input_scale, q, sf);
-  else
-    hipLaunchKernelGGL(rmsnorm_quant_kernel<false>, dim3(M), dim3(256), 0, s, x, w, out, H, eps, 1.f / input_scale, q,
-                       nullptr);
+  if (nvfp4) rmsnorm_launch<true>(M, H, s, x, w, out, eps, 1.f / input_scale, q, sf);
+  else rmsnorm_launch<false>(M, H, s, x, w, out, eps, 1.f / input_scale, q, nullptr);
   return check_launch("rmsnorm_quant");
 }
 

@@ -316,27 +316,44 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
   }
 }
 
-// 1x128 FP8 activation quantizer: one wave per (row, 128-value group); s = amax / 448 (1 for an all-zero
-// group), q = E4M3(x / s) rounded to nearest even (|x / s| <= 448 by construction; clamped for safety, which
-// is the saturating conversion). Two values per lane.
+// 1x128 FP8 activation quantizer: 16 lanes per (row, 128-value group), eight values (16 bytes) per lane, so a
+// wave covers four groups with 16-byte loads and 8-byte stores; s = amax / 448 (1 for an all-zero group),
+// q = E4M3(x / s) rounded to nearest even (|x / s| <= 448 by construction; clamped for safety, which is the
+// saturating conversion).
 __global__ void __launch_bounds__(256) quant_fp8_g128_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                              uint8_t* __restrict__ q, float* __restrict__ scale) {
   const int KB = K / 128;
-  const long long grp = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
-  if (grp >= static_cast<long long>(M) * KB) return;
-  const int m = static_cast<int>(grp / KB), kb = static_cast<int>(grp % KB);
-  const size_t base = static_cast<size_t>(m) * K + static_cast<size_t>(kb) * 128 + 2 * lane;
-  const uint32_t pair = *reinterpret_cast<const uint32_t*>(x + base);
-  const float v0 = bf16_to_f32(pair & 0xffff), v1 = bf16_to_f32(pair >> 16);
-  float mx = fmaxf(fabsf(v0), fabsf(v1));
+  const long long grp = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+  const int sub = threadIdx.x & 15;
+  const bool ok = grp < static_cast<long long>(M) * KB;  // the 16 lanes of a group agree
+  const int m = ok ? static_cast<int>(grp / KB) : 0, kb = ok ? static_cast<int>(grp % KB) : 0;
+  const size_t base = static_cast<size_t>(m) * K + static_cast<size_t>(kb) * 128 + 8 * sub;
+  u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+  if (ok) raw = *reinterpret_cast<const u32x4*>(x + base);
+  float v[8];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16_to_f32(raw[i] & 0xffff);
+    v[2 * i + 1] = bf16_to_f32(raw[i] >> 16);
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
   const float s = mx > 0.f ? mx / 448.f : 1.f;
-  const float a0 = fminf(fmaxf(v0 / s, -448.f), 448.f), a1 = fminf(fmaxf(v1 / s, -448.f), 448.f);
-  const uint32_t packed = __builtin_amdgcn_cvt_pk_fp8_f32(a0, a1, 0, false);
-  *reinterpret_cast<uint16_t*>(q + base) = static_cast<uint16_t>(packed & 0xffff);
-  if (lane == 0) scale[static_cast<size_t>(m) * KB + kb] = s;
+  uint32_t w[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = fminf(fmaxf(v[4 * h + i] / s, -448.f), 448.f);
+    const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0, false);
+    w[h] = __builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], lo, true);
+  }
+  if (!ok) return;
+  *reinterpret_cast<u32x2*>(q + base) = u32x2{w[0], w[1]};
+  if (sub == 0) scale[static_cast<size_t>(m) * KB + kb] = s;
 }
 
 // Per-tensor FP8 activation quantizer (reference src/core/prefill_gemm.cu:496-511): each value rounded to BF16
@@ -418,8 +435,10 @@ extern "C" {
 int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* scale, void* stream) {
   if (M < 1 || K <= 0 || K % 128 != 0) return fail(LQ_ERR_SHAPE, "quant_act_fp8_g128: M >= 1 and K % 128 == 0");
   if (!x || !q || !scale) return fail(LQ_ERR_ARG, "quant_act_fp8_g128: null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q) % 8 != 0)
+    return fail(LQ_ERR_ARG, "quant_act_fp8_g128: x must be 16-byte and q 8-byte aligned");
   const long long groups = static_cast<long long>(M) * (K / 128);
-  hipLaunchKernelGGL(quant_fp8_g128_kernel, dim3(static_cast<unsigned>((groups + 3) / 4)), dim3(256), 0,
+  hipLaunchKernelGGL(quant_fp8_g128_kernel, dim3(static_cast<unsigned>((groups + 15) / 16)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, M, K, q, scale);
   return check_launch("quant_act_fp8_g128");
 }

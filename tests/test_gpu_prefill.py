@@ -356,3 +356,53 @@ def test_prefill_swiglu_nvfp4(L):
         uc, ur = L.retile_nvfp4_coded(to_dev(uv_), to_dev(us_), to_dev(c2))
         q2, sf2 = L.prefill_swiglu_nvfp4(to_dev(xq), to_dev(xs), gc, ag, uc, au, N, osc, gate_sf=gr, up_sf=ur)
         assert np.array_equal(q2.cpu().numpy(), qd) and np.array_equal(sf2.cpu().numpy(), sfd)
+
+
+def test_rmsnorm_quant_row_widths(L):
+    """Rows of 1024 (one wave), 20480 (two blocks a thread) and 65536 (four) values, and the limit beyond."""
+    for H in (1024, 20480, 65536):
+        x = O.normal_f32(43, 2.0, (3, H))
+        w = O.normal_bf16(44, 0.2, (H,))
+        out, q, sf = L.rmsnorm_quant(to_dev(x), to_dev(w.view(np.int16)), 1e-6, True, 0.01)
+        ref_out, _, _ = O.rmsnorm_quant(x, w, 1e-6, True, 0.01)
+        outd = out.cpu().numpy()
+        assert np.max(np.abs(outd - ref_out)) <= 4e-6 * np.max(np.abs(ref_out)), H
+        rq, rsf = O.quant_act_nvfp4(outd, 0.01)
+        assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(sf.cpu().numpy(), rsf), H
+    w = torch.zeros((66560,), dtype=torch.int16, device=DEV)
+    with pytest.raises(L.LingGemmError, match="at most 65536"):
+        L.rmsnorm_quant(torch.zeros((1, 66560), dtype=torch.float32, device=DEV), w, 1e-6, True, 1.0)
+
+
+def test_quant_act_fp8_g128_rounding_boundaries(L):
+    """Quotients x / s on and next to E4M3 rounding midpoints (the quantizer's reciprocal shortcut must fall back to
+    the division there): groups with s = 3 exactly (amax 1344) holding 3 x every midpoint of [2^-9, 448], groups
+    with an inexact s (amax 1000) holding the BF16 values nearest to midpoint x s and their BF16 neighbours, and
+    groups of tiny and huge magnitudes."""
+    codes = np.arange(0, 0x7f, dtype=np.uint8)
+    vals = np.array([_e4m3(c) for c in codes], np.float32)
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2)
+    rows = []
+    for amax, scale in ((1344.0, 3.0), (1000.0, 1000.0 / 448.0)):
+        tgt = np.concatenate([mids, -mids]) * scale
+        b = O.f32_to_bf16(tgt.astype(np.float32))
+        nb = np.concatenate([b, b + 1, b - 1]).astype(np.uint16)
+        nb = nb[np.abs(O.bf16_to_f32(nb)) <= amax]
+        n = -(-len(nb) // 127) * 127
+        nb = np.resize(nb, n).reshape(-1, 127)
+        head = np.full((nb.shape[0], 1), O.f32_to_bf16(np.array([amax], np.float32))[0], np.uint16)
+        rows.append(np.concatenate([head, nb], axis=1))
+    g = np.concatenate(rows).reshape(-1)
+    tiny = O.normal_bf16(71, 1e-30, (1, 128)).reshape(-1)
+    huge = O.normal_bf16(72, 1e30, (1, 128)).reshape(-1)
+    g = np.concatenate([g, tiny, huge])
+    x = np.resize(g, -(-g.size // 1024) * 1024).reshape(-1, 1024)
+    q, s = L.quant_act_fp8_g128(bf16_dev(x))
+    wq, ws = O.quant_act_fp8_g128(x)
+    assert np.array_equal(s.cpu().numpy(), ws)
+    assert np.array_equal(q.cpu().numpy(), wq)
+
+
+def _e4m3(c):
+    e, m = (int(c) >> 3) & 15, int(c) & 7
+    return (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
