@@ -97,6 +97,17 @@ static_assert(sizeof(StreamArgs) <= 320 && offsetof(StreamArgs, x) / 64 == 0 &&
                   (offsetof(StreamArgs, tg0) + 4 * sizeof(int)) / 64 == 4,
               "argument lines touched at kernel entry");
 
+// arr[mi] of an argument array, read as constant-offset argument loads and a select: no argument read waits on
+// mi (or on another argument read), so the reads of a prologue or an epilogue batch into one scalar round trip
+// instead of a chain of dependent ones.
+template <int N, class X>
+__device__ __forceinline__ X pick(const X (&arr)[N], int mi) {
+  X v = arr[0];
+#pragma unroll
+  for (int k = 1; k < kMaxMats; ++k) v = mi == k ? arr[k] : v;
+  return v;
+}
+
 // Phase stamps of a workgroup for builds with LQ_STREAM_TRACE: kept in registers, written once at exit.
 // 0 entry, 1 first chunk computed, 2 stream done, 3 partials published, 4 arrival counted, 5 reduced, 6 exit,
 // 7 prologue loads issued, 8 first partial added, 9 reduction loop done, 10 arguments read, 11 tiles set up,
@@ -232,16 +243,19 @@ __device__ __forceinline__ void epi_load(const StreamArgs& a, int mi, int wtile0
   for (int i = 0; i < T; ++i) {
     const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
     const int n = epi_row<PAIR, T>(wtile0, i, t);
-    const float sc = a.sc[m];
+    const float sc = pick(a.sc, m);
+    const float* const svec = pick(a.svec, m);
+    const uint16_t* const resid = pick(a.resid, m);
+    const int Nm = pick(a.N, m), ldy = pick(a.ldy, m);
     e.sv[i] = f32x4{sc, sc, sc, sc};
-    if (a.svec[m] && n < a.N[m]) e.sv[i] = *reinterpret_cast<const f32x4*>(a.svec[m] + n);
+    if (svec && n < Nm) e.sv[i] = *reinterpret_cast<const f32x4*>(svec + n);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const int tok = 16 * g + r;
       e.rr[i][g] = u32x2{0u, 0u};
       if constexpr (!PAIR && !OUTF32) {
-        if (a.resid[m] && tok < a.M && n < a.N[m])
-          e.rr[i][g] = *reinterpret_cast<const u32x2*>(a.resid[m] + static_cast<size_t>(tok) * a.ldy[m] + n);
+        if (resid && tok < a.M && n < Nm)
+          e.rr[i][g] = *reinterpret_cast<const u32x2*>(resid + static_cast<size_t>(tok) * ldy + n);
       }
     }
   }
@@ -282,28 +296,31 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
           *reinterpret_cast<u32x2*>(dst) = pk;
       }
     } else {
+      const int Nm = pick(a.N, mi), ldy = pick(a.ldy, mi);
+      void* const y = pick(a.y, mi);
+      const uint16_t* const resid = pick(a.resid, mi);
 #pragma unroll
       for (int i = 0; i < T; ++i) {
         const int n = epi_row<PAIR, T>(wtile0, i, t);
-        if (n >= a.N[mi]) continue;
+        if (n >= Nm) continue;
         float vv[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           vv[v] = acc[i][g][v] * e.sv[i][v];
           if (a.xinv) vv[v] = vv[v] * e.xi[g];
         }
-        const size_t o = static_cast<size_t>(tok) * a.ldy[mi] + n;
+        const size_t o = static_cast<size_t>(tok) * ldy + n;
         if constexpr (OUTF32) {
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.y[mi]) + o) = f32x4{vv[0], vv[1], vv[2], vv[3]};
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + o) = f32x4{vv[0], vv[1], vv[2], vv[3]};
         } else {
-          if (a.resid[mi]) {
+          if (resid) {
             const u32x2 rr = e.rr[i][g];
             vv[0] = vv[0] + bf16_to_f32(rr.x & 0xffff);
             vv[1] = vv[1] + bf16_to_f32(rr.x >> 16);
             vv[2] = vv[2] + bf16_to_f32(rr.y & 0xffff);
             vv[3] = vv[3] + bf16_to_f32(rr.y >> 16);
           }
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.y[mi]) + o) =
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + o) =
               u32x2{f32_to_bf16(vv[0]) | (uint32_t(f32_to_bf16(vv[1])) << 16),
                     f32_to_bf16(vv[2]) | (uint32_t(f32_to_bf16(vv[3])) << 16)};
         }
@@ -327,20 +344,24 @@ struct SegTiles {
 
 template <int WF, int T, bool PAIR>
 __device__ __forceinline__ void seg_tiles(const StreamArgs& a, int tg, int wave, SegTiles<WF, T, PAIR>& s) {
+  // the matrix of tile group tg: the last mi < count with tg0[mi] <= tg (tg0 is increasing), counted without a
+  // loop whose argument reads would wait on each other
   int mi = 0;
   if constexpr (!PAIR) {
-    while (mi + 1 < a.count && tg >= a.tg0[mi + 1]) ++mi;
+#pragma unroll
+    for (int k = 1; k < kMaxMats; ++k) mi += (k < a.count && tg >= a.tg0[k]) ? 1 : 0;
   }
   s.mi = mi;
-  s.wtile0 = (tg - a.tg0[mi]) * (group_rows(T, PAIR) / 16) + wave * (PAIR ? T / 2 : T);
+  s.wtile0 = (tg - pick(a.tg0, mi)) * (group_rows(T, PAIR) / 16) + wave * (PAIR ? T / 2 : T);
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const int m = PAIR ? (i < T / 2 ? 0 : 1) : mi;
-    const int tile = min((PAIR ? s.wtile0 + (i % (T / 2)) : s.wtile0 + i), a.N[m] / 16 - 1);
+    const int Nm = pick(a.N, m);
+    const int tile = min((PAIR ? s.wtile0 + (i % (T / 2)) : s.wtile0 + i), Nm / 16 - 1);
     const int blk = WF == kFp8 ? kTileBytesFp8 : WF == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
-    s.rs[i] = make_rsrc(a.w[m]);
+    s.rs[i] = make_rsrc(pick(a.w, m));
     s.toff[i] = tile * a.C * blk;
-    s.coff[i] = (a.N[m] / 16) * a.C * kValueBytesFp4 + tile * a.C * kCodeBytesFp4;
+    s.coff[i] = (Nm / 16) * a.C * kValueBytesFp4 + tile * a.C * kCodeBytesFp4;
   }
 }
 
