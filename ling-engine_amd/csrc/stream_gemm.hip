@@ -1526,13 +1526,13 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.cap = cap;
   a.N = N;
   a.y = y;
-  // the full launch's split (stream_launch for this N, K): tile groups of group_rows(4) rows (NVFP4 always runs
-  // four tiles per wave)
-  a.TGR = group_rows(tiles_per_wave(kFp4, false), false);
-  const long long units = static_cast<long long>(cdiv(N, a.TGR)) * a.C;
-  a.P = choose_wgs(units);
-  if (units * (a.P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, nm + ": matrix too large");
-  a.U = static_cast<int>(units);
+  // the full launch's split (choose_tiles for this N, K): its tiles per wave, tile groups, workgroups and units
+  StreamArgs full{};
+  full.C = a.C;
+  if (int rc = choose_tiles(nm.c_str(), kFp4, false, &N, 1, full)) return rc;
+  a.TGR = group_rows(full.T, false);
+  a.P = full.P;
+  a.U = full.U;
   const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cdiv(M, 16)) {

@@ -305,11 +305,12 @@ def test_stream_gemm_gather_nvfp4_bit_exact(L, N, K):
                 assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"gather M={M} count={c}"
 
 
-def test_stream_nvfp4_bf16(L):
+@pytest.mark.parametrize("N,K", [(512, 2560), (8192, 2560)])
+def test_stream_nvfp4_bf16(L, N, K):
     """BF16 activations on the NVFP4 path: each 128-value chunk of a row is staged as FP16 under its own
     power-of-two scale. Rows span 1e-6 .. 3e4 in magnitude, chunks within a row differ by up to 2^12, one row is
-    zero; every M is row-invariant against M = 68, raw and coded scales agree."""
-    N, K = 512, 2560
+    zero; every M is row-invariant against M = 68, raw and coded scales agree. Two shapes: a tile group spread
+    over 20 workgroups' ranges (512 rows) and over 8 (8192 rows)."""
     w = O.normal_bf16(16, 0.02, (N, K))
     v, s, g, _ = O.quant_nvfp4(w)
     tw = L.retile_nvfp4(to_dev(v), to_dev(s))
