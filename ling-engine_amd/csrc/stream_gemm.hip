@@ -395,12 +395,14 @@ __device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
 // workgroup order. Every workgroup (the finisher included) published its partial before arriving, so all of
 // them are read back from memory, D partials of each group per batch: a batch's loads (of both groups, when
 // this workgroup finishes its first and its last tile group) are all issued before its adds, so a fan-in of up
-// to D costs one memory round trip.
+// to D costs one memory round trip. D is 16 (8 per group when finishing two) for four accumulator vectors at
+// one or two tiles per wave: the FP8 kernels' fan-in of up to 8 then takes one round trip. At four NVFP4 tiles
+// per wave the deeper batch measured slower, so it stays at 8.
 template <int G, int T, int NG>
 __device__ __forceinline__ void reduce_partials(const StreamArgs& a, const SplitInfo* si, f32x4 (*acc[NG])[G], int r,
                                                 unsigned long long (&ts)[16]) {
   constexpr int NV = T * G;  // accumulator vectors per thread
-  constexpr int D0 = NV <= 4 ? 8 : NV <= 8 ? 4 : NV <= 10 ? 3 : NV <= 16 ? 2 : 1;
+  constexpr int D0 = NV <= 4 ? (T <= 2 ? 16 : 8) : NV <= 8 ? 4 : NV <= 10 ? 3 : NV <= 16 ? 2 : 1;
   constexpr int D = NG == 2 ? (D0 + 1) / 2 : D0;
   const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
   int n[NG];
