@@ -397,11 +397,13 @@ def cpu_baseline(O):
                       f"{best * threads:.1f} core-seconds"}
 
 
-def bench_producers(torch, L, args, dev):
+def bench_producers(torch, L, dev):
     """The activation producers at config 4's shapes (M = 4096 tokens) and the sparse-head gather (M = 17, 2048
     of 151936 vocabulary rows of a 5120-wide NVFP4 head): all HBM-bound, so each reports its bytes moved (inputs
     read once, outputs written once), the time per launch (HIP events over back-to-back launches rotating over
-    input copies of >= 1 GB) and the fraction of 8 TB/s."""
+    input copies of >= 1 GB) and the fraction of 8 TB/s. The gather's eight row sets touch 48 MB of the head, which
+    the 256 MB MALL can hold across repetitions; the gather is latency-bound either way (timed alike with rows in
+    order or repeated)."""
     M, H, F = 4096, 5120, 17408
     g = torch.Generator(device=dev)
     g.manual_seed(0x4C51000A)
@@ -506,7 +508,7 @@ def main():
         extra["prefill_nvfp4_m4096"] = pn
         log(f"[bench] prefill nvfp4: {pn}")
     if only is None or "producers" in only:
-        pr = bench_producers(torch, L, args, dev)
+        pr = bench_producers(torch, L, dev)
         extra["producers"] = pr
         log(f"[bench] producers: {pr}")
     if args.copy_calibration:
