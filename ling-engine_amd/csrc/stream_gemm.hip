@@ -530,13 +530,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   constexpr int PF = pf_stages<T>(G);
   constexpr bool BPRE = Smem<G>::BPRE;
   constexpr int NSLOT = Smem<G>::NSLOT;
-#ifdef LQ_EXP_PLAIN
-  constexpr bool YCOH = false, XCOH = (MODE & kXCoh) != 0;
-  constexpr int XPOL = 0;
-#else
   constexpr bool YCOH = (MODE & kYCoh) != 0, XCOH = (MODE & kXCoh) != 0;
   constexpr int XPOL = XCOH ? kSc1 : 0;
-#endif
   constexpr bool CVT = (MODE & kCvt) != 0;
   static_assert(!CVT || F16, "converted activations feed the FP16 MFMA");
   static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
