@@ -440,6 +440,18 @@ def bench_producers(torch, L, dev):
     w = (torch.randn(H, device=dev, generator=g) * 0.1).to(torch.bfloat16).view(torch.int16)
     out["rmsnorm_quant_nvfp4"] = line("rmsq", byt + 2 * H, timed(
         lambda i: L.rmsnorm_quant(xf[i], w, 1e-6, True, 0.01, with_out=False), c))
+    # per-tensor FP8 quantizer and RMSNorm into FP8: FP32 in, FP8 out
+    out["quant_act_fp8"] = line("fp8", 5 * nb, timed(lambda i: L.quant_act_fp8(xf[i], 0.02), c))
+    out["rmsnorm_quant_fp8"] = line("rmsq8", 5 * nb + 2 * H, timed(
+        lambda i: L.rmsnorm_quant(xf[i], w, 1e-6, False, 0.02, with_out=False), c))
+    # the stream GEMMs' FP16 activation copies, at the largest skinny M (68 rows; latency-bound at this size):
+    # FP32 in, FP16 + per-row scale out (RMSNorm also writes FP32)
+    ms_ = 68
+    xs68 = [xf[i][:ms_].contiguous() for i in range(c)]
+    n68 = ms_ * H
+    out["to_half_rows_m68"] = line("half", 6 * n68 + 4 * ms_, timed(lambda i: L.to_half_rows(xs68[i]), c))
+    out["rmsnorm_half_m68"] = line("rmsh", 10 * n68 + 4 * ms_ + 2 * H, timed(
+        lambda i: L.rmsnorm_half(xs68[i], w.view(torch.bfloat16), 1e-6), c))
     del xf
     # silu(g) * u into NVFP4 (the FFN's gate|up outputs, FP32): two inputs
     nf = M * F
