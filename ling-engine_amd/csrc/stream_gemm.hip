@@ -39,6 +39,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <type_traits>
 #include <utility>
 
 namespace lq {
@@ -1130,6 +1131,40 @@ __global__ void __launch_bounds__(256) half_rows_kernel(const void* __restrict__
   if (blockIdx.y == 0 && threadIdx.x == 0) xinv[m] = ldexpf(1.f, e - 15);
 }
 
+// The same with one block per row and the row held in registers (NPT values per thread, thread t holding values
+// t + 256 j): one read of the row, whose loads are all issued before the maximum is taken. Same arithmetic per
+// element as half_rows_kernel. Rows up to 256 * NPT values.
+template <bool BF16IN, int NPT>
+__global__ void __launch_bounds__(256) half_rows_reg_kernel(const void* __restrict__ x, int K,
+                                                            _Float16* __restrict__ out, float* __restrict__ xinv) {
+  __shared__ float red[4];
+  const size_t m = blockIdx.x;
+  float v[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int k = static_cast<int>(threadIdx.x) + 256 * j;
+    if constexpr (BF16IN) v[j] = k < K ? bf16_to_f32(reinterpret_cast<const uint16_t*>(x)[m * K + k]) : 0.f;
+    else v[j] = k < K ? reinterpret_cast<const float*>(x)[m * K + k] : 0.f;
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) mx = fmaxf(mx, fabsf(v[j]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.f && isfinite(mx)) frexpf(mx, &e);
+  const float s = ldexpf(1.f, 15 - e);
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int k = static_cast<int>(threadIdx.x) + 256 * j;
+    if (k < K) out[m * K + k] = static_cast<_Float16>(v[j] * s);
+  }
+  if (threadIdx.x == 0) xinv[m] = ldexpf(1.f, e - 15);
+}
+
 // RMSNorm of each row into FP32 `out` and the FP16 row copy the stream GEMM reads (reference
 // src/core/stream_gemm.cu:380-418): rstd = 1 / sqrt(sum(x^2) / H + eps), v = x * rstd * w' with w' = 1 + w
 // (Gemma) or w, then xh = f16_rn(v * 2^(15 - e)), xinv = 2^(e - 15) from the row's largest |v| (the values
@@ -1169,6 +1204,62 @@ __global__ void __launch_bounds__(256) rmsnorm_half_kernel(const float* __restri
   if (mx > 0.f && isfinite(mx)) frexpf(mx, &e);
   const float sc = ldexpf(1.f, 15 - e);
   for (int h = tid; h < H; h += 256) xh[r * H + h] = static_cast<_Float16>(val(h) * sc);
+  if (tid == 0) xinv[r] = ldexpf(1.f, e - 15);
+}
+
+// The same with the row and its weights held in registers (NPT values per thread, thread t holding values
+// t + 256 j): one read of each, the same sum order (h ascending per thread) and the same arithmetic per element
+// as rmsnorm_half_kernel. Rows up to 256 * NPT values.
+template <int NPT>
+__global__ void __launch_bounds__(256) rmsnorm_half_reg_kernel(const float* __restrict__ x,
+                                                               const uint16_t* __restrict__ w, float* __restrict__ out,
+                                                               _Float16* __restrict__ xh, float* __restrict__ xinv,
+                                                               int H, float eps, bool gemma) {
+  __shared__ float red[4];
+  const size_t r = blockIdx.x;
+  const float* row = x + r * H;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  float v[NPT], wf[NPT];
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int h = tid + 256 * j;
+    v[j] = h < H ? row[h] : 0.f;
+    wf[j] = h < H ? bf16_to_f32(w[h]) : 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j)
+    if (tid + 256 * j < H) ss += v[j] * v[j];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if (lane == 0) red[wv] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float rstd = 1.f / sqrtf(tot / static_cast<float>(H) + eps);
+  float mx = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int h = tid + 256 * j;
+    if (h < H) {
+      v[j] = v[j] * rstd * (gemma ? 1.f + wf[j] : wf[j]);
+      out[r * H + h] = v[j];
+      mx = fmaxf(mx, fabsf(v[j]));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  __syncthreads();
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (mx > 0.f && isfinite(mx)) frexpf(mx, &e);
+  const float sc = ldexpf(1.f, 15 - e);
+#pragma unroll
+  for (int j = 0; j < NPT; ++j) {
+    const int h = tid + 256 * j;
+    if (h < H) xh[r * H + h] = static_cast<_Float16>(v[j] * sc);
+  }
   if (tid == 0) xinv[r] = ldexpf(1.f, e - 15);
 }
 
@@ -1386,6 +1477,21 @@ int half_rows(bool bf16in, const void* x, int M, int K, uint16_t* xh, float* xin
   const char* nm = bf16in ? "bf16_to_half_rows" : "to_half_rows";
   if (M < 1 || K < 1) return fail(LQ_ERR_SHAPE, std::string(nm) + ": M and K must be positive");
   if (!x || !xh || !xinv) return fail(LQ_ERR_ARG, std::string(nm) + ": null pointer");
+  // rows of up to 8192 values: one block per row, the row in registers
+  auto reg = [&](auto npt) {
+    constexpr int NPT = decltype(npt)::value;
+    if (bf16in)
+      hipLaunchKernelGGL((half_rows_reg_kernel<true, NPT>), dim3(M), dim3(256), 0, s, x, K,
+                         reinterpret_cast<_Float16*>(xh), xinv);
+    else
+      hipLaunchKernelGGL((half_rows_reg_kernel<false, NPT>), dim3(M), dim3(256), 0, s, x, K,
+                         reinterpret_cast<_Float16*>(xh), xinv);
+    return check_launch(nm);
+  };
+  if (K <= 1024) return reg(std::integral_constant<int, 4>{});
+  if (K <= 2048) return reg(std::integral_constant<int, 8>{});
+  if (K <= 4096) return reg(std::integral_constant<int, 16>{});
+  if (K <= 8192) return reg(std::integral_constant<int, 32>{});
   const int split = std::max(1, std::min(K / 1024, cdiv(192, M)));
   const int slice = cdiv(K, split);
   const dim3 grid(M, cdiv(K, slice));
@@ -1423,8 +1529,14 @@ int lq_rmsnorm_half(const float* x, const uint16_t* w, float* out, uint16_t* xh,
                     int gemma, void* stream) {
   if (rows < 1 || H < 1) return fail(LQ_ERR_SHAPE, "rmsnorm_half: rows and H must be positive");
   if (!x || !w || !out || !xh || !xinv) return fail(LQ_ERR_ARG, "rmsnorm_half: null pointer");
-  hipLaunchKernelGGL(rmsnorm_half_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), x, w, out,
-                     reinterpret_cast<_Float16*>(xh), xinv, H, eps, gemma != 0);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  _Float16* const xh16 = reinterpret_cast<_Float16*>(xh);
+  // rows of up to 8192 values: the row and its weights in registers
+  if (H <= 1024) hipLaunchKernelGGL(rmsnorm_half_reg_kernel<4>, dim3(rows), dim3(256), 0, s, x, w, out, xh16, xinv, H, eps, gemma != 0);
+  else if (H <= 2048) hipLaunchKernelGGL(rmsnorm_half_reg_kernel<8>, dim3(rows), dim3(256), 0, s, x, w, out, xh16, xinv, H, eps, gemma != 0);
+  else if (H <= 4096) hipLaunchKernelGGL(rmsnorm_half_reg_kernel<16>, dim3(rows), dim3(256), 0, s, x, w, out, xh16, xinv, H, eps, gemma != 0);
+  else if (H <= 8192) hipLaunchKernelGGL(rmsnorm_half_reg_kernel<32>, dim3(rows), dim3(256), 0, s, x, w, out, xh16, xinv, H, eps, gemma != 0);
+  else hipLaunchKernelGGL(rmsnorm_half_kernel, dim3(rows), dim3(256), 0, s, x, w, out, xh16, xinv, H, eps, gemma != 0);
   return check_launch("rmsnorm_half");
 }
 

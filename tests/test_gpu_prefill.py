@@ -198,7 +198,8 @@ def test_prefill_per_tensor_config4_rows(L):
 
 
 # ---------------- rmsnorm_half (reference stream_gemm.cu:380-418) ----------------
-@pytest.mark.parametrize("rows,H,gemma", [(1, 5120, True), (17, 5120, True), (3, 17408, False), (68, 1024, True)])
+@pytest.mark.parametrize("rows,H,gemma", [(1, 5120, True), (17, 5120, True), (3, 17408, False), (68, 1024, True),
+                                         (2, 3000, False)])
 def test_rmsnorm_half(L, rows, H, gemma):
     x = O.normal_f32(80 + rows, 2.0, (rows, H))
     w = O.normal_bf16(81 + rows, 0.1, (H,))

@@ -216,6 +216,17 @@ def test_to_half_rows_bit_exact(L):
     assert np.array_equal(binv.cpu().numpy(), winv2)
 
 
+@pytest.mark.parametrize("K", [100, 1000, 3000, 8192])
+def test_to_half_rows_row_widths(L, K):
+    """Rows held in registers (up to 8192 values a row), including widths that leave a ragged tail."""
+    x = O.normal_f32(13 + K, 1.0, (5, K))
+    x[4] = 0
+    xh, xinv = L.to_half_rows(to_dev(x))
+    wh, winv = O.to_half_rows(x)
+    assert np.array_equal(xh.view(torch.int16).cpu().numpy().view(np.uint16), wh)
+    assert np.array_equal(xinv.cpu().numpy(), winv)
+
+
 def reference_style_weights(seed, N, K):
     """tests/stream_tests.cu:147-160: random bytes (no E4M3 NaN), NVFP4 scales 0x28..0x48, x with outliers."""
     rng = np.random.default_rng(seed)
