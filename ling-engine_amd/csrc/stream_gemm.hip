@@ -1477,7 +1477,7 @@ int half_rows(bool bf16in, const void* x, int M, int K, uint16_t* xh, float* xin
   const char* nm = bf16in ? "bf16_to_half_rows" : "to_half_rows";
   if (M < 1 || K < 1) return fail(LQ_ERR_SHAPE, std::string(nm) + ": M and K must be positive");
   if (!x || !xh || !xinv) return fail(LQ_ERR_ARG, std::string(nm) + ": null pointer");
-  // rows of up to 8192 values: one block per row, the row in registers
+  // rows of up to 32768 values: one block per row, the row in registers
   auto reg = [&](auto npt) {
     constexpr int NPT = decltype(npt)::value;
     if (bf16in)
@@ -1492,6 +1492,8 @@ int half_rows(bool bf16in, const void* x, int M, int K, uint16_t* xh, float* xin
   if (K <= 2048) return reg(std::integral_constant<int, 8>{});
   if (K <= 4096) return reg(std::integral_constant<int, 16>{});
   if (K <= 8192) return reg(std::integral_constant<int, 32>{});
+  if (K <= 16384) return reg(std::integral_constant<int, 64>{});
+  if (K <= 32768) return reg(std::integral_constant<int, 128>{});
   const int split = std::max(1, std::min(K / 1024, cdiv(192, M)));
   const int slice = cdiv(K, split);
   const dim3 grid(M, cdiv(K, slice));

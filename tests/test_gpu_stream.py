@@ -216,9 +216,9 @@ def test_to_half_rows_bit_exact(L):
     assert np.array_equal(binv.cpu().numpy(), winv2)
 
 
-@pytest.mark.parametrize("K", [100, 1000, 3000, 8192])
+@pytest.mark.parametrize("K", [100, 1000, 3000, 8192, 12000, 32768])
 def test_to_half_rows_row_widths(L, K):
-    """Rows held in registers (up to 8192 values a row), including widths that leave a ragged tail."""
+    """Rows held in registers (up to 32768 values a row), including widths that leave a ragged tail."""
     x = O.normal_f32(13 + K, 1.0, (5, K))
     x[4] = 0
     xh, xinv = L.to_half_rows(to_dev(x))
