@@ -146,8 +146,10 @@ int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const 
 int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate, const uint8_t* w_up,
                          const float* s_up, const uint8_t* w_down, const float* s_down, const uint16_t* resid,
                          uint16_t* h, uint16_t* y, int I, int H, void* stream);
-/* Synchronous: *hit = 1 if a stream_fp8_pc_ffn launch on the current device ever gave up its in-kernel wait at
- * the deadline (its results are then not valid), else 0. No counterpart in the reference (its wait traps). */
+/* Synchronous: *hit = 1 if a stream_fp8_pc_ffn launch on the current device gave up its in-kernel wait at the
+ * deadline since the last call (the results of such a launch are not valid), else 0; the call clears the flag.
+ * A caller of lq_stream_fp8_pc_ffn that cannot rule out a concurrent kernel holding CUs checks it after
+ * synchronizing. No counterpart in the reference (its wait traps). */
 int lq_stream_ffn_deadline_status(int* hit);
 /* y[M][N] = bf16(scale2 * x . W^T), W tiled NVFP4 (raw, or coded with its device table), x BF16. The kernel
  * turns each 128-value chunk of a row of x into FP16 under a power-of-two scale from that chunk's largest
@@ -183,6 +185,11 @@ int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float 
 int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
                      float input_scale, uint8_t* q, uint8_t* sf, void* stream);
 
+/* rmsnorm_quant with the FP32 copy replaced by a BF16 one (out BF16 [M][H], may be null): out = bf16(v), the same
+ * rounding the quantizer applies. kernels.cuh:234-235 rmsnorm_quant_bf16 */
+int lq_rmsnorm_quant_bf16(const float* x, const uint16_t* w, uint16_t* out, int M, int H, float eps, int nvfp4,
+                          float input_scale, uint8_t* q, uint8_t* sf, void* stream);
+
 /* ---------------- prefill, block-scaled FP8 (additive; reference src/core/kernels.cuh:190-221) ---------------- */
 /* BF16 x [M][K] -> FP8 E4M3 q [M][K] with one FP32 scale per 1x128 group, scale [M][K/128] = amax / 448 (1 for an
  * all-zero group), q = E4M3_rne(x / scale); x 16-byte and q 8-byte aligned. The block-scaled counterpart of
@@ -199,6 +206,9 @@ int lq_prefill_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_
 /* FP32 x [M][K] -> FP8 E4M3 q = E4M3_satfinite(bf16(x) * (1 / input_scale)). K % 4 == 0.
  * kernels.cuh:199 quant_act_fp8 */
 int lq_quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q, void* stream);
+/* quant_act_fp8 over a BF16 copy x [M][K] (8-byte aligned): the bytes the FP32 values it was rounded from give.
+ * kernels.cuh:237 quant_act_fp8_bf16in */
+int lq_quant_act_fp8_bf16in(const uint16_t* x, int M, int K, float input_scale, uint8_t* q, void* stream);
 /* y[M][0..N) (FP32, rows ldy apart) = alpha * xq . W^T, or += with accumulate; W tiled FP8. N % 128 == 0,
  * K % 128 == 0; M < 1 does nothing. kernels.cuh:213-214 prefill_gemm_fp8 */
 int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
@@ -206,6 +216,24 @@ int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha,
 /* The same rounded to BF16 (never accumulated). kernels.cuh:239-240 prefill_gemm_fp8_bf16out */
 int lq_prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, float alpha, uint16_t* y, int ldy, int N,
                                 int K, void* stream);
+
+/* ---------------- host weight quantizers (CPU threads; host pointers) ----------------
+ * High-precision weights [N][K] (row-major) into the formats the GEMMs read, before lq_retile_* / the weight file.
+ * E4M3 is OCP E4M3FN: round to nearest even, saturating to +-448. */
+enum { LQ_DT_F32 = 0, LQ_DT_BF16 = 1, LQ_DT_F16 = 2 };
+/* NVFP4 round-to-nearest of BF16 weights: *scale2 = g = amax / (448 * 6) (1 if all zero); scales [N][K/16] =
+ * E4M3(max(amax16 / 6 / g, 2^-9)); values [N][K/2] (low nibble first) = the E2M1 code of the magnitude nearest to
+ * w / (e4m3(scale) * g), ties to the smaller, sign only on non-zero codes. rel_sq_err (may be NULL) = sum of
+ * squared errors / sum of squares. K % 16 == 0. Reference src/core/model.cu:188-249 quantize_nvfp4 (model.hpp:41). */
+int lq_quantize_nvfp4(const uint16_t* w_bf16, int N, int K, uint8_t* values, uint8_t* scales, float* scale2,
+                      double* rel_sq_err);
+/* FP8 with one FP32 scale per output channel: scale [N] = max(amax_n / 448, 1e-12), q [N][K] = E4M3(w / scale).
+ * Reference bench/quant/drafter_variants.py:77-81 fake_fp8 (the per-channel recipe of the benchmark configs). */
+int lq_quantize_fp8_channel(const void* w, int dtype, int N, int K, uint8_t* q, float* scale);
+/* FP8 in 128 x 128 blocks (the block-scaled prefill's weights): scale [ceil(N/128)][ceil(K/128)] = amax / 448
+ * (1 for an all-zero block), q [N][K] = E4M3(w / scale). No reference counterpart (the reference's prefill is
+ * per-tensor FP8, src/core/prefill_gemm.cu:4-7); the format of lq_prefill_fp8_block's ws. */
+int lq_quantize_fp8_block128(const void* w, int dtype, int N, int K, uint8_t* q, float* scale);
 
 /* ---------------- the on-disk kernel-order weight file (host only; no GPU is used) ----------------
  * The offline step the reference's README names ("ling-compile") and never built: its load path maps the
@@ -224,9 +252,18 @@ int lq_prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w, floa
  * other tensor is copied as is (LQ_WENTRY_RAW). N % 16 == 0 and K % 128 == 0 for every quantized weight. */
 #define LQ_WFILE_NO_CODES 1
 #define LQ_WFILE_PASSTHROUGH 2
+/* Quantize high-precision linears while compiling (at most one of these): every 2-D P.weight in BF16, F16 or F32
+ * with no scale tensors, N % 16 == 0, K % 128 == 0 and a name containing neither "embed" nor "norm" becomes an FP8
+ * per-channel (lq_quantize_fp8_channel), FP8 128x128-block (lq_quantize_fp8_block128) or NVFP4
+ * (lq_quantize_nvfp4, F16 / F32 rounded to BF16 first) entry, marked LQ_WENTRY_QUANTIZED; the reference quantizes
+ * such matrices at load (src/core/model.cu:188-249, src/core/drafter.cpp:93-100). */
+#define LQ_WFILE_QUANT_FP8 4
+#define LQ_WFILE_QUANT_FP8_BLOCK 8
+#define LQ_WFILE_QUANT_NVFP4 16
 enum { LQ_WENTRY_FP8 = 1, LQ_WENTRY_NVFP4 = 2, LQ_WENTRY_NVFP4_CODED = 3, LQ_WENTRY_RAW = 4 };
 enum { LQ_WSCALE_NONE = 0, LQ_WSCALE_TENSOR = 1, LQ_WSCALE_CHANNEL = 2, LQ_WSCALE_BLOCK128 = 3 };
 #define LQ_WENTRY_HAS_INPUT_SCALE 1
+#define LQ_WENTRY_QUANTIZED 2 /* quantized by the compiler from the checkpoint dtype in `dtype` */
 
 typedef struct lq_wfile lq_wfile;
 typedef struct {

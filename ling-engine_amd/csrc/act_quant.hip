@@ -75,9 +75,11 @@ __global__ void __launch_bounds__(256) quant_nvfp4_kernel(const float* __restric
 // order, then the wave, then the waves in order), rstd = 1 / sqrt(sum / H + eps), v = x * rstd * (1 + w)
 // (written to `out` when given), then the thread quantizes its blocks of BF16(v): NVFP4, or FP8
 // E4M3(BF16(v) / input_scale).
-template <bool FP4, int NB>
+// BF16OUT: `out` is BF16, the values rounded as the quantizer rounds them (reference rmsnorm_quant_bf16,
+// prefill_gemm.cu:640-645, the norm_quant_kernel's OutT = BF16 form).
+template <bool FP4, int NB, bool BF16OUT>
 __global__ void __launch_bounds__(1024) rmsnorm_quant_kernel(const float* __restrict__ x, const uint16_t* __restrict__ w,
-                                                             float* __restrict__ out, int H, float eps, float g,
+                                                             void* __restrict__ out, int H, float eps, float g,
                                                              uint8_t* __restrict__ q, uint8_t* __restrict__ sf) {
   __shared__ float red[16];
   const size_t r = blockIdx.x;
@@ -120,10 +122,20 @@ __global__ void __launch_bounds__(1024) rmsnorm_quant_kernel(const float* __rest
         const uint32_t wb = (h & 1) ? wp[h >> 1] >> 16 : wp[h >> 1] & 0xffff;
         v[h] = f[j][k][e] * rstd * (1.f + bf16_to_f32(wb));
       }
-      if (out) reinterpret_cast<f32x4*>(out + r * H)[blk * 4 + k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+      if (out && !BF16OUT)
+        reinterpret_cast<f32x4*>(static_cast<float*>(out) + r * H)[blk * 4 + k] =
+            f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
     }
+    uint32_t ob[8];
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) ob[i >> 1] = f32_to_bf16(v[i]) | (uint32_t(f32_to_bf16(v[i + 1])) << 16);
 #pragma unroll
     for (int i = 0; i < 16; ++i) v[i] = bf16_round(v[i]);
+    if (out && BF16OUT) {
+      u32x4* o = reinterpret_cast<u32x4*>(static_cast<uint16_t*>(out) + r * H + static_cast<size_t>(blk) * 16);
+      o[0] = u32x4{ob[0], ob[1], ob[2], ob[3]};
+      o[1] = u32x4{ob[4], ob[5], ob[6], ob[7]};
+    }
     const size_t b = r * nblk + blk;
     if constexpr (FP4) {
       put_nvfp4_block(v, g, q + b * 8, sf + b);
@@ -140,15 +152,39 @@ __global__ void __launch_bounds__(1024) rmsnorm_quant_kernel(const float* __rest
   }
 }
 
-template <bool FP4>
-void rmsnorm_launch(int M, int H, hipStream_t s, const float* x, const uint16_t* w, float* out, float eps, float g,
+template <bool FP4, bool BF16OUT>
+void rmsnorm_launch(int M, int H, hipStream_t s, const float* x, const uint16_t* w, void* out, float eps, float g,
                     uint8_t* q, uint8_t* sf) {
   const int nblk = H / 16;
   const int T = nblk < 1024 ? nblk : 1024;  // H % 1024 == 0: a multiple of 64
   const int nb = (nblk + T - 1) / T;
-  if (nb == 1) hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 1>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
-  else if (nb == 2) hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 2>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
-  else hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 4>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+  if (nb == 1)
+    hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 1, BF16OUT>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+  else if (nb == 2)
+    hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 2, BF16OUT>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+  else hipLaunchKernelGGL((rmsnorm_quant_kernel<FP4, 4, BF16OUT>), dim3(M), dim3(T), 0, s, x, w, out, H, eps, g, q, sf);
+}
+
+int rmsnorm_quant_any(const char* name, const float* x, const uint16_t* w, void* out, bool bf16out, int M, int H,
+                      float eps, int nvfp4, float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
+  const std::string nm(name);
+  if (M < 1) return fail(LQ_ERR_SHAPE, nm + ": M must be positive");
+  if (H <= 0 || H % 1024 != 0) return fail(LQ_ERR_SHAPE, nm + ": H % 1024 must be 0");
+  if (H > 65536) return fail(LQ_ERR_SHAPE, nm + ": H must be at most 65536 (the row is held in registers)");
+  if (!x || !w || !q || (nvfp4 && !sf)) return fail(LQ_ERR_ARG, nm + ": null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(q)) % 16 != 0)
+    return fail(LQ_ERR_ARG, nm + ": x, w, out and q must be 16-byte aligned");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const float g = 1.f / input_scale;
+  if (nvfp4) {
+    if (bf16out) rmsnorm_launch<true, true>(M, H, s, x, w, out, eps, g, q, sf);
+    else rmsnorm_launch<true, false>(M, H, s, x, w, out, eps, g, q, sf);
+  } else {
+    if (bf16out) rmsnorm_launch<false, true>(M, H, s, x, w, out, eps, g, q, nullptr);
+    else rmsnorm_launch<false, false>(M, H, s, x, w, out, eps, g, q, nullptr);
+  }
+  return check_launch(name);
 }
 
 unsigned grid_for(size_t items) {
@@ -188,17 +224,12 @@ int lq_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float 
 
 int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
                      float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
-  if (M < 1) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: M must be positive");
-  if (H <= 0 || H % 1024 != 0) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: H % 1024 must be 0");
-  if (H > 65536) return fail(LQ_ERR_SHAPE, "rmsnorm_quant: H must be at most 65536 (the row is held in registers)");
-  if (!x || !w || !q || (nvfp4 && !sf)) return fail(LQ_ERR_ARG, "rmsnorm_quant: null pointer");
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out) |
-       reinterpret_cast<uintptr_t>(q)) % 16 != 0)
-    return fail(LQ_ERR_ARG, "rmsnorm_quant: x, w, out and q must be 16-byte aligned");
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (nvfp4) rmsnorm_launch<true>(M, H, s, x, w, out, eps, 1.f / input_scale, q, sf);
-  else rmsnorm_launch<false>(M, H, s, x, w, out, eps, 1.f / input_scale, q, nullptr);
-  return check_launch("rmsnorm_quant");
+  return rmsnorm_quant_any("rmsnorm_quant", x, w, out, false, M, H, eps, nvfp4, input_scale, q, sf, stream);
+}
+
+int lq_rmsnorm_quant_bf16(const float* x, const uint16_t* w, uint16_t* out, int M, int H, float eps, int nvfp4,
+                          float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
+  return rmsnorm_quant_any("rmsnorm_quant_bf16", x, w, out, true, M, H, eps, nvfp4, input_scale, q, sf, stream);
 }
 
 }  // extern "C"

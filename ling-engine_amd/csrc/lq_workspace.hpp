@@ -15,7 +15,8 @@ struct Workspace {
   int* counters = nullptr;
   size_t counter_count = 0;
   int* sync = nullptr;
-  bool external = false;  // partials, counters and sync live in a caller-owned buffer (lq_set_workspace)  // [16] one-launch FFN: phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
+  bool external = false;  // partials, counters and sync live in a caller-owned buffer (lq_set_workspace)
+  // sync[16]: the one-launch FFN's phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
   // prefill tail split: FP32 partial tiles and per-tile arrival counters (zeroed once, self-resetting)
   float* pf_partials = nullptr;
   size_t pf_partial_bytes = 0;
@@ -30,5 +31,7 @@ struct Workspace {
 
 // The calling thread's current device's workspace (created on first call), or null (error set).
 Workspace* workspace_for_current_device();
+// Reserves the prefill's tail-split scratch at its bound (one FP32 tile per CU, one counter per CU), once.
+int reserve_prefill_scratch(Workspace* ws);
 
 }  // namespace lq

@@ -359,14 +359,28 @@ __global__ void __launch_bounds__(256) quant_fp8_g128_kernel(const uint16_t* __r
 // Per-tensor FP8 activation quantizer (reference src/core/prefill_gemm.cu:496-511): each value rounded to BF16
 // first (production's activations are BF16), times 1 / input_scale, then E4M3 with saturation to +-448 (NaN
 // stays NaN). Four values per thread.
-__global__ void __launch_bounds__(256) quant_fp8_pt_kernel(const float* __restrict__ x, size_t quads, float inv_scale,
+// BF16IN: x holds BF16 values (reference quant_act_fp8_bf16in, prefill_gemm.cu:626-630): the same bytes as from the
+// FP32 values they were rounded from.
+template <bool BF16IN>
+__global__ void __launch_bounds__(256) quant_fp8_pt_kernel(const void* __restrict__ x, size_t quads, float inv_scale,
                                                            uint8_t* __restrict__ q) {
   for (size_t i = blockIdx.x * static_cast<size_t>(256) + threadIdx.x; i < quads; i += static_cast<size_t>(gridDim.x) * 256) {
-    const f32x4 f = reinterpret_cast<const f32x4*>(x)[i];
+    float f[4];
+    if constexpr (BF16IN) {
+      const u32x2 h = reinterpret_cast<const u32x2*>(x)[i];
+      f[0] = __uint_as_float(h.x << 16);
+      f[1] = __uint_as_float(h.x & 0xffff0000u);
+      f[2] = __uint_as_float(h.y << 16);
+      f[3] = __uint_as_float(h.y & 0xffff0000u);
+    } else {
+      const f32x4 v4 = reinterpret_cast<const f32x4*>(x)[i];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) f[k] = bf16_to_f32(f32_to_bf16(v4[k]));
+    }
     float v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float b = bf16_to_f32(f32_to_bf16(f[k])) * inv_scale;
+      const float b = f[k] * inv_scale;
       v[k] = isnan(b) ? b : fminf(fmaxf(b, -448.f), 448.f);
     }
     const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
@@ -408,10 +422,11 @@ int prefill_launch(PrefillArgs a, const char* name, hipStream_t s) {
   a.full = static_cast<int>(tiles - a.rem);
   const long long blocks = a.full + (a.rem ? 8LL * cdiv(a.rem, 8) * a.S : 0);
   if (a.rem) {
+    // rem * S <= P partial tiles: the bound is reserved once per device (lq_init, or here on first use) and never
+    // reallocated, so a graph captured with these pointers stays valid whatever shapes run later
     Workspace* ws = workspace_for_current_device();
     if (!ws) return LQ_ERR_DEVICE;
-    const int rc = ws->reserve_prefill(static_cast<size_t>(a.rem) * a.S * kBN * kBM * sizeof(float),
-                                       static_cast<size_t>(a.rem));
+    const int rc = reserve_prefill_scratch(ws);
     if (rc) return rc;
     a.part = ws->pf_partials;
     a.cnt = ws->pf_counters;
@@ -426,6 +441,14 @@ int prefill_launch(PrefillArgs a, const char* name, hipStream_t s) {
 }
 
 }  // namespace
+
+int reserve_prefill_scratch(Workspace* ws) {
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const size_t P = static_cast<size_t>(device_cus(dev));
+  return ws->reserve_prefill(P * kBN * kBM * sizeof(float), P);
+}
+
 }  // namespace lq
 
 using namespace lq;
@@ -465,9 +488,21 @@ int lq_quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q
     return fail(LQ_ERR_ARG, "quant_act_fp8: x must be 16-byte and q 4-byte aligned");
   const size_t quads = static_cast<size_t>(M) * K / 4;
   const unsigned grid = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 256 * 64));
-  hipLaunchKernelGGL(quant_fp8_pt_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), x, quads,
+  hipLaunchKernelGGL(quant_fp8_pt_kernel<false>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), x, quads,
                      1.f / input_scale, q);
   return check_launch("quant_act_fp8");
+}
+
+int lq_quant_act_fp8_bf16in(const uint16_t* x, int M, int K, float input_scale, uint8_t* q, void* stream) {
+  if (M < 1 || K <= 0 || K % 4 != 0) return fail(LQ_ERR_SHAPE, "quant_act_fp8_bf16in: M >= 1 and K % 4 == 0");
+  if (!x || !q) return fail(LQ_ERR_ARG, "quant_act_fp8_bf16in: null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 8 != 0 || reinterpret_cast<uintptr_t>(q) % 4 != 0)
+    return fail(LQ_ERR_ARG, "quant_act_fp8_bf16in: x must be 8-byte and q 4-byte aligned");
+  const size_t quads = static_cast<size_t>(M) * K / 4;
+  const unsigned grid = static_cast<unsigned>(std::min<size_t>((quads + 255) / 256, 256 * 64));
+  hipLaunchKernelGGL(quant_fp8_pt_kernel<true>, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream), x, quads,
+                     1.f / input_scale, q);
+  return check_launch("quant_act_fp8_bf16in");
 }
 
 int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,

@@ -87,26 +87,28 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
   return LQ_OK;
 }
 
+// Allocated once, at the bound the caller passes (reserve_prefill_scratch), and never reallocated: a graph captured
+// with these pointers must stay valid.
 int Workspace::reserve_prefill(size_t bytes, size_t counters_needed) {
   std::lock_guard<std::mutex> lock(g_mutex);
-  if (bytes > pf_partial_bytes) {
-    if (pf_partials) (void)hipFree(pf_partials);
+  if (pf_partials) {
+    if (bytes > pf_partial_bytes || counters_needed > pf_counter_count)
+      return fail(LQ_ERR_DEVICE, "workspace: prefill split scratch is smaller than its bound");
+    return LQ_OK;
+  }
+  if (hipMalloc(&pf_partials, bytes) != hipSuccess) {
     pf_partials = nullptr;
-    pf_partial_bytes = 0;
-    if (hipMalloc(&pf_partials, bytes) != hipSuccess)
-      return fail(LQ_ERR_DEVICE, "workspace: prefill partial buffer allocation failed");
-    pf_partial_bytes = bytes;
+    return fail(LQ_ERR_DEVICE, "workspace: prefill partial buffer allocation failed");
   }
-  if (counters_needed > pf_counter_count) {
-    const size_t cap = std::max(counters_needed, size_t(4096));
-    if (pf_counters) (void)hipFree(pf_counters);
+  if (hipMalloc(&pf_counters, counters_needed * sizeof(int)) != hipSuccess ||
+      hipMemset(pf_counters, 0, counters_needed * sizeof(int)) != hipSuccess) {
+    (void)hipFree(pf_partials);
+    pf_partials = nullptr;
     pf_counters = nullptr;
-    pf_counter_count = 0;
-    if (hipMalloc(&pf_counters, cap * sizeof(int)) != hipSuccess ||
-        hipMemset(pf_counters, 0, cap * sizeof(int)) != hipSuccess)
-      return fail(LQ_ERR_DEVICE, "workspace: prefill counter allocation failed");
-    pf_counter_count = cap;
+    return fail(LQ_ERR_DEVICE, "workspace: prefill counter allocation failed");
   }
+  pf_partial_bytes = bytes;
+  pf_counter_count = counters_needed;
   return LQ_OK;
 }
 
@@ -172,6 +174,8 @@ int lq_init(void) {
   lq::Workspace* ws = lq::workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
   int rc = ws->external ? LQ_OK : ws->reserve_stream(size_t(64) << 20, size_t(1) << 16);
+  if (rc) return rc;
+  rc = lq::reserve_prefill_scratch(ws);
   if (rc) return rc;
   return hipDeviceSynchronize() == hipSuccess ? LQ_OK : lq::fail(LQ_ERR_DEVICE, "lq_init: device synchronize failed");
 }

@@ -899,12 +899,14 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
   stream_body<G, kFp8, 2, false, true, false, kYCoh>(a, p, sm, NoWait{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores have completed
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // release: this workgroup's h stores (ordered before the add by the barrier) are visible device-wide before
+  // its arrival is; the pollers' acquire pairs with it
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   const int P = a.P;
   auto ready = [&]() {
     if (threadIdx.x == 0) {
       const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-      while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < P) {
+      while (__hip_atomic_load(sync, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < P) {
         __builtin_amdgcn_s_sleep(2);
         if (__builtin_amdgcn_s_memrealtime() - t0 > kFfnDeadlineTicks) {
           __hip_atomic_store(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1664,6 +1666,11 @@ int lq_stream_ffn_deadline_status(int* hit) {
   if (!ws->sync) return LQ_OK;
   if (hipMemcpy(hit, ws->sync + 2, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
     return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: copy failed");
+  if (*hit) {  // reading clears it: a later report names only launches after this one
+    const int zero = 0;
+    if (hipMemcpy(ws->sync + 2, &zero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+      return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: clear failed");
+  }
   return LQ_OK;
 }
 

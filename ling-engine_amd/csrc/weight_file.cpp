@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "ling_gemm.h"
+#include "lq_quantize.hpp"
 
 namespace lq {
 int fail(int code, const std::string& msg);
@@ -580,6 +581,94 @@ void set_dtype(Entry& e, const std::string& d) {
   std::memcpy(e.dtype, d.data(), std::min(d.size(), sizeof e.dtype - 1));
 }
 
+constexpr int kQuantFlags = LQ_WFILE_QUANT_FP8 | LQ_WFILE_QUANT_FP8_BLOCK | LQ_WFILE_QUANT_NVFP4;
+
+// A high-precision linear weight quantized here (LQ_WFILE_QUANT_*): a 2-D P.weight in BF16, F16 or F32 with no
+// scale tensors of its own, N % 16 == 0 and K % 128 == 0, and a name naming neither an embedding nor a norm (those
+// are lookups and vectors, not GEMM operands). Anything else is left to the passthrough. NVFP4 takes BF16 values
+// (the reference's quantize_nvfp4, src/core/model.cu:188-249, rounds BF16): F16 and F32 weights are rounded to
+// BF16 first. FP8 quantizes the exact FP32 values.
+void plan_quantized(const Checkpoint& ck, const std::string& name, const std::string& prefix, const Tensor& w,
+                    int flags, std::vector<Plan>& plans, std::set<std::string>& consumed) {
+  int dt;
+  if (w.dtype == "BF16") dt = LQ_DT_BF16;
+  else if (w.dtype == "F16") dt = LQ_DT_F16;
+  else if (w.dtype == "F32") dt = LQ_DT_F32;
+  else return;
+  if (w.shape.size() != 2 || ck.find(prefix + ".weight_scale") || ck.find(prefix + ".weight_scale_inv")) return;
+  if (name.find("embed") != std::string::npos || name.find("norm") != std::string::npos) return;
+  if (w.shape[0] <= 0 || w.shape[1] <= 0 || w.shape[0] > (int64_t(1) << 30) || w.shape[1] > (int64_t(1) << 29)) return;
+  const int N = static_cast<int>(w.shape[0]), K = static_cast<int>(w.shape[1]);
+  if (N % 16 != 0 || K % kChunk != 0) return;
+  Plan p;
+  p.name = prefix;
+  Entry& e = p.e;
+  e.N = N;
+  e.K = K;
+  e.ndim = 2;
+  e.shape[0] = N;
+  e.shape[1] = K;
+  e.flags |= LQ_WENTRY_QUANTIZED;
+  set_dtype(e, w.dtype);
+  const Tensor* in = ck.find(prefix + ".input_scale");
+  if (in) {
+    e.input_scale = scalar_f32(*in, prefix + ".input_scale");
+    e.flags |= LQ_WENTRY_HAS_INPUT_SCALE;
+    consumed.insert(prefix + ".input_scale");
+  }
+  consumed.insert(name);
+  const uint8_t* src = w.data;
+  if (flags & LQ_WFILE_QUANT_NVFP4) {
+    // BF16 values (rounded once here for F16 / F32), then the scales now: whether the blob is coded depends on them
+    auto bf = std::make_shared<std::vector<uint16_t>>();
+    const void* vals = src;
+    if (dt != LQ_DT_BF16) {
+      bf->resize(size_t(N) * K);
+      for (size_t i = 0; i < bf->size(); ++i) (*bf)[i] = lq::hostq::f32_to_bf16(lq::hostq::element(src, dt, i));
+      vals = bf->data();
+    }
+    auto scl = std::make_shared<std::vector<uint8_t>>(size_t(N) * K / 16);
+    const float g = lq::hostq::nvfp4_scales(vals, LQ_DT_BF16, N, K, scl->data());
+    e.weight_scale = g;
+    uint8_t table[64], code_of[256];
+    const bool coded = !(flags & LQ_WFILE_NO_CODES) && lq_scale_code_table(scl->data(), scl->size(), table, code_of) == 1;
+    if (coded) {
+      e.kind = LQ_WENTRY_NVFP4_CODED;
+      e.blob_bytes = lq_tiled_bytes_nvfp4_coded(N, K);
+      e.aux_bytes = size_t(N) * K / 16;
+      e.table_bytes = 64;
+    } else {
+      e.kind = LQ_WENTRY_NVFP4;
+      e.blob_bytes = lq_tiled_bytes_nvfp4(N, K);
+    }
+    std::vector<uint8_t> tab(table, table + 64), map(code_of, code_of + 256);
+    p.fill = [=](uint8_t* blob, uint8_t* aux, uint8_t* tb) {
+      std::vector<uint8_t> v(size_t(N) * K / 2);
+      (void)lq::hostq::nvfp4_values(vals, LQ_DT_BF16, N, K, g, scl->data(), v.data());
+      (void)bf;  // keeps the BF16 copy alive until the values are made
+      if (coded) {
+        host_retile_nvfp4_coded(v.data(), scl->data(), map.data(), blob, aux, N, K);
+        std::memcpy(tb, tab.data(), 64);
+      } else {
+        host_retile_nvfp4_values(v.data(), scl->data(), blob, 1152, nullptr, N, K);
+      }
+    };
+  } else {
+    const bool block = (flags & LQ_WFILE_QUANT_FP8_BLOCK) != 0;
+    e.kind = LQ_WENTRY_FP8;
+    e.blob_bytes = lq_tiled_bytes_fp8(N, K);
+    e.scale_kind = block ? LQ_WSCALE_BLOCK128 : LQ_WSCALE_CHANNEL;
+    e.aux_bytes = block ? size_t((N + 127) / 128) * ((K + 127) / 128) * 4 : size_t(N) * 4;
+    p.fill = [=](uint8_t* blob, uint8_t* aux, uint8_t*) {
+      std::vector<uint8_t> q(size_t(N) * K);
+      if (block) lq::hostq::fp8_block128(src, dt, N, K, q.data(), reinterpret_cast<float*>(aux));
+      else lq::hostq::fp8_channel(src, dt, N, K, q.data(), reinterpret_cast<float*>(aux));
+      host_retile_fp8(q.data(), blob, N, K);
+    };
+  }
+  plans.push_back(std::move(p));
+}
+
 std::vector<Plan> plan_checkpoint(const Checkpoint& ck, int flags, std::set<std::string>& consumed) {
   std::vector<Plan> plans;
   const std::string suffix = ".weight";
@@ -591,7 +680,10 @@ std::vector<Plan> plan_checkpoint(const Checkpoint& ck, int flags, std::set<std:
     const Tensor* ws = ck.find(prefix + ".weight_scale");
     const bool nvfp4 = w.dtype == "U8" && ws && ws->dtype == "F8_E4M3";
     const bool fp8 = w.dtype == "F8_E4M3";
-    if (!nvfp4 && !fp8) continue;
+    if (!nvfp4 && !fp8) {
+      if (flags & kQuantFlags) plan_quantized(ck, name, prefix, w, flags, plans, consumed);
+      continue;
+    }
     if (w.shape.size() != 2) throw ArgError(name + ": a quantized weight must be 2-D");
     // N and K are int in the kernels' interface (and K = 2 x the packed NVFP4 width)
     if (w.shape[0] > (int64_t(1) << 30) || w.shape[1] > (int64_t(1) << 29))
@@ -811,6 +903,27 @@ struct lq_wfile {
 
 namespace {
 
+// The section sizes a GEMM will read for this entry's kind and shape: a blob shorter than its tiled size would make
+// a GEMM read past the mapping.
+bool sizes_match(const Entry& e) {
+  if (e.kind == LQ_WENTRY_RAW) return true;
+  if (e.N <= 0 || e.K <= 0 || e.N % 16 != 0 || e.K % kChunk != 0) return false;
+  const size_t N = size_t(e.N), K = size_t(e.K);
+  switch (e.kind) {
+    case LQ_WENTRY_FP8: {
+      size_t aux = 0;
+      if (e.scale_kind == LQ_WSCALE_CHANNEL) aux = N * 4;
+      else if (e.scale_kind == LQ_WSCALE_BLOCK128) aux = ((N + 127) / 128) * ((K + 127) / 128) * 4;
+      else if (e.scale_kind != LQ_WSCALE_TENSOR && e.scale_kind != LQ_WSCALE_NONE) return false;
+      return e.blob_bytes == lq_tiled_bytes_fp8(e.N, e.K) && e.aux_bytes == aux && e.table_bytes == 0;
+    }
+    case LQ_WENTRY_NVFP4:
+      return e.blob_bytes == lq_tiled_bytes_nvfp4(e.N, e.K) && e.aux_bytes == 0 && e.table_bytes == 0;
+    default:  // coded NVFP4
+      return e.blob_bytes == lq_tiled_bytes_nvfp4_coded(e.N, e.K) && e.aux_bytes == N * K / 16 && e.table_bytes == 64;
+  }
+}
+
 lq_wfile* open_file(const std::string& path) {
   auto f = std::make_unique<lq_wfile>();
   f->map = std::make_unique<Mapping>(path, true);
@@ -823,8 +936,10 @@ lq_wfile* open_file(const std::string& path) {
   if (h.version != kVersion) throw IoError(path + ": unsupported version " + std::to_string(h.version));
   if (h.file_bytes != n) throw IoError(path + ": truncated or padded (" + std::to_string(n) + " bytes, header says " +
                                        std::to_string(h.file_bytes) + ")");
-  if (h.entries_off != sizeof(FileHeader) || h.strings_off != h.entries_off + uint64_t(h.count) * sizeof(Entry) ||
-      h.strings_off + h.strings_bytes > h.data_off || h.data_off > n)
+  // every sum below is checked against the mapped size before it is formed, so a crafted header cannot wrap
+  if (h.entries_off != sizeof(FileHeader) || h.count > (n - sizeof(FileHeader)) / sizeof(Entry) ||
+      h.strings_off != h.entries_off + uint64_t(h.count) * sizeof(Entry) || h.data_off > n ||
+      h.strings_off > h.data_off || h.strings_bytes > h.data_off - h.strings_off)
     throw IoError(path + ": bad section offsets");
   if (hash64(d + h.entries_off, h.strings_off + h.strings_bytes - h.entries_off) != h.meta_hash)
     throw IoError(path + ": entry table hash mismatch");
@@ -833,11 +948,13 @@ lq_wfile* open_file(const std::string& path) {
   auto in_data = [&](uint64_t off, uint64_t bytes) { return bytes == 0 || (off >= h.data_off && off <= n && bytes <= n - off); };
   for (uint32_t i = 0; i < h.count; ++i) {
     const Entry& e = f->entries[i];
-    if (e.name_off + e.name_len + 1 > h.strings_bytes || f->strings[e.name_off + e.name_len] != '\0')
+    if (e.name_off >= h.strings_bytes || e.name_len >= h.strings_bytes - e.name_off ||
+        f->strings[e.name_off + e.name_len] != '\0')
       throw IoError(path + ": bad name of entry " + std::to_string(i));
     if (!in_data(e.blob_off, e.blob_bytes) || !in_data(e.aux_off, e.aux_bytes) || !in_data(e.table_off, e.table_bytes))
       throw IoError(path + ": section of entry " + std::to_string(i) + " is out of the file");
     if (e.kind < LQ_WENTRY_FP8 || e.kind > LQ_WENTRY_RAW) throw IoError(path + ": bad kind of entry " + std::to_string(i));
+    if (!sizes_match(e)) throw IoError(path + ": section sizes of entry " + std::to_string(i) + " do not fit its shape");
     f->index[std::string(f->strings + e.name_off, e.name_len)] = static_cast<int>(i);
   }
   return f.release();
@@ -893,7 +1010,9 @@ int lq_host_retile_nvfp4_coded(const uint8_t* w, const uint8_t* wscale, const ui
 int lq_wfile_compile(const char* checkpoint_dir, const char* out_path, int flags, int* entries_written) {
   return guarded([&] {
     if (!checkpoint_dir || !out_path) throw ArgError("wfile_compile: null path");
-    if (flags & ~(LQ_WFILE_NO_CODES | LQ_WFILE_PASSTHROUGH)) throw ArgError("wfile_compile: unknown flags");
+    if (flags & ~(LQ_WFILE_NO_CODES | LQ_WFILE_PASSTHROUGH | kQuantFlags)) throw ArgError("wfile_compile: unknown flags");
+    const int q = flags & kQuantFlags;
+    if (q & (q - 1)) throw ArgError("wfile_compile: at most one LQ_WFILE_QUANT_* flag");
     compile_file(checkpoint_dir, out_path, flags, entries_written);
     return LQ_OK;
   });

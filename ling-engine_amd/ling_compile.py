@@ -6,7 +6,12 @@ every load (src/core/model.cu:131-186). Here `compile_checkpoint` runs the libra
 (lq_wfile_compile: CPU threads, no GPU) and `WeightFile` maps the result; `WeightFile.load` copies an
 entry's sections to device memory, ready for the GEMM entry points of ling_gemm.
 
-    python ling-engine_amd/ling_compile.py CHECKPOINT_DIR OUT.lqw [--no-codes] [--passthrough] [--list]
+    python ling-engine_amd/ling_compile.py CHECKPOINT_DIR OUT.lqw [--no-codes] [--passthrough]
+        [--quantize {fp8,fp8-block,nvfp4}] [--list]
+
+--quantize also turns high-precision (BF16 / F16 / F32) linear weights into FP8 per-channel, FP8 128x128-block or
+NVFP4 entries with the library's host quantizers, as the reference's loader does for its NVFP4 copies
+(src/core/model.cu:188-249).
 """
 from __future__ import annotations
 
@@ -21,9 +26,13 @@ import torch
 import ling_gemm as L
 
 
-def compile_checkpoint(checkpoint_dir: str, out_path: str, codes: bool = True, passthrough: bool = False) -> int:
+QUANTIZE = {None: 0, "fp8": L.WFILE_QUANT_FP8, "fp8-block": L.WFILE_QUANT_FP8_BLOCK, "nvfp4": L.WFILE_QUANT_NVFP4}
+
+
+def compile_checkpoint(checkpoint_dir: str, out_path: str, codes: bool = True, passthrough: bool = False,
+                       quantize: str | None = None) -> int:
     """Compile checkpoint_dir into out_path; returns the number of entries written."""
-    flags = (0 if codes else L.WFILE_NO_CODES) | (L.WFILE_PASSTHROUGH if passthrough else 0)
+    flags = (0 if codes else L.WFILE_NO_CODES) | (L.WFILE_PASSTHROUGH if passthrough else 0) | QUANTIZE[quantize]
     n = C.c_int(0)
     L._check(L.lib.lq_wfile_compile(checkpoint_dir.encode(), out_path.encode(), flags, C.byref(n)))
     return n.value
@@ -41,6 +50,7 @@ class Entry:
     input_scale: float | None
     dtype: str
     shape: tuple
+    quantized: bool
     blob: np.ndarray
     aux: np.ndarray | None
     table: np.ndarray | None
@@ -111,7 +121,7 @@ class WeightFile:
                      weight_scale=e.weight_scale,
                      input_scale=e.input_scale if e.flags & L.WENTRY_HAS_INPUT_SCALE else None,
                      dtype=e.dtype.decode(), shape=tuple(e.shape[d] for d in range(e.ndim)),
-                     blob=_view(e.blob, e.blob_bytes), aux=aux, table=_view(e.table, e.table_bytes))
+                     quantized=bool(e.flags & L.WENTRY_QUANTIZED), blob=_view(e.blob, e.blob_bytes), aux=aux, table=_view(e.table, e.table_bytes))
 
     def verify(self, key) -> None:
         i = self.index(key) if isinstance(key, str) else int(key)
@@ -143,9 +153,11 @@ def main(argv=None) -> int:
     ap.add_argument("out")
     ap.add_argument("--no-codes", action="store_true", help="write NVFP4 weights raw, never scale-coded")
     ap.add_argument("--passthrough", action="store_true", help="copy every non-quantized tensor too")
+    ap.add_argument("--quantize", choices=["fp8", "fp8-block", "nvfp4"],
+                    help="quantize high-precision linear weights into this format")
     ap.add_argument("--list", action="store_true", help="print the entries written")
     a = ap.parse_args(argv)
-    n = compile_checkpoint(a.checkpoint, a.out, codes=not a.no_codes, passthrough=a.passthrough)
+    n = compile_checkpoint(a.checkpoint, a.out, codes=not a.no_codes, passthrough=a.passthrough, quantize=a.quantize)
     print(f"{a.out}: {n} entries")
     if a.list:
         with WeightFile(a.out) as f:

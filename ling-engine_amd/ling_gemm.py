@@ -55,6 +55,8 @@ SIGNATURES = {
     "lq_prefill_fp8_block": (_I, [_P, _P, _I, _P, _P, _P, _I, _I, _I, _P]),
     "lq_rmsnorm_half": (_I, [_P, _P, _P, _P, _P, _I, _I, _F, _I, _P]),
     "lq_quant_act_fp8": (_I, [_P, _I, _I, _F, _P, _P]),
+    "lq_quant_act_fp8_bf16in": (_I, [_P, _I, _I, _F, _P, _P]),
+    "lq_rmsnorm_quant_bf16": (_I, [_P, _P, _P, _I, _I, _F, _I, _F, _P, _P, _P]),
     "lq_prefill_gemm_fp8": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _I, _P]),
     "lq_prefill_gemm_fp8_bf16out": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _P]),
     "lq_wfile_compile": (_I, [C.c_char_p, C.c_char_p, _I, _P]),
@@ -67,10 +69,16 @@ SIGNATURES = {
     "lq_host_retile_fp8": (_I, [_P, _P, _I, _I]),
     "lq_host_retile_nvfp4": (_I, [_P, _P, _P, _I, _I]),
     "lq_host_retile_nvfp4_coded": (_I, [_P, _P, _P, _P, _P, _I, _I]),
+    "lq_quantize_nvfp4": (_I, [_P, _I, _I, _P, _P, _P, _P]),
+    "lq_quantize_fp8_channel": (_I, [_P, _I, _I, _I, _P, _P]),
+    "lq_quantize_fp8_block128": (_I, [_P, _I, _I, _I, _P, _P]),
 }
 
 # include/ling_gemm.h lq_wentry / lq_wfile flags and kinds
 WFILE_NO_CODES, WFILE_PASSTHROUGH = 1, 2
+WFILE_QUANT_FP8, WFILE_QUANT_FP8_BLOCK, WFILE_QUANT_NVFP4 = 4, 8, 16
+WENTRY_QUANTIZED = 2
+DT_F32, DT_BF16, DT_F16 = 0, 1, 2
 WENTRY_FP8, WENTRY_NVFP4, WENTRY_NVFP4_CODED, WENTRY_RAW = 1, 2, 3, 4
 WSCALE_NONE, WSCALE_TENSOR, WSCALE_CHANNEL, WSCALE_BLOCK128 = 0, 1, 2, 3
 WENTRY_HAS_INPUT_SCALE = 1
@@ -428,6 +436,17 @@ def rmsnorm_quant(x, w_bf16, eps: float, nvfp4: bool, input_scale: float, with_o
     return out, q, sf
 
 
+def rmsnorm_quant_bf16(x, w_bf16, eps: float, nvfp4: bool, input_scale: float, with_out: bool = True):
+    """-> (out BF16 or None, q, sf or None)."""
+    M, H = x.shape
+    out = torch.empty((M, H), dtype=torch.bfloat16, device=x.device) if with_out else None
+    q = torch.empty((M, H // 2) if nvfp4 else (M, H), dtype=torch.uint8, device=x.device)
+    sf = torch.empty((M, H // 16), dtype=torch.uint8, device=x.device) if nvfp4 else None
+    _check(lib.lq_rmsnorm_quant_bf16(_ptr(_dev(x, torch.float32)), _ptr(_dev(w_bf16)), _ptr(out), M, H, eps,
+                                     int(nvfp4), input_scale, _ptr(q), _ptr(sf), _stream()))
+    return out, q, sf
+
+
 # ---------------- prefill ----------------
 def quant_act_fp8_g128(x):
     M, K = x.shape
@@ -453,6 +472,13 @@ def quant_act_fp8(x, input_scale: float):
     return q
 
 
+def quant_act_fp8_bf16in(x, input_scale: float):
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.uint8, device=x.device)
+    _check(lib.lq_quant_act_fp8_bf16in(_ptr(_dev(x, torch.bfloat16)), M, K, input_scale, _ptr(q), _stream()))
+    return q
+
+
 def prefill_gemm_fp8(xq, w, alpha: float, N: int, y=None, ldy: int | None = None, accumulate: bool = False):
     M, K = xq.shape
     ldy = N if ldy is None else ldy
@@ -469,3 +495,51 @@ def prefill_gemm_fp8_bf16out(xq, w, alpha: float, N: int, y=None, ldy: int | Non
     _check(lib.lq_prefill_gemm_fp8_bf16out(_ptr(_dev(xq, torch.uint8)), M, _ptr(w), alpha,
                                            _ptr(_dev(y, torch.bfloat16)), ldy, N, K, _stream()))
     return y
+
+
+# ---------------- host weight quantizers (numpy arrays on the host) ----------------
+def _host_w(w):
+    import numpy as np
+    w = np.ascontiguousarray(w)
+    if w.dtype == np.float32:
+        return w, DT_F32
+    if w.dtype == np.float16:
+        return w, DT_F16
+    if w.dtype == np.uint16:  # BF16 bit patterns
+        return w, DT_BF16
+    raise TypeError("weights must be float32, float16 or uint16 (BF16 bits)")
+
+
+def quantize_nvfp4(w_bf16):
+    """BF16 bits [N][K] -> (values [N][K/2], scales [N][K/16], scale2, rel_sq_err) (reference model.cu:188-249)."""
+    import numpy as np
+    w = np.ascontiguousarray(w_bf16, np.uint16)
+    N, K = w.shape
+    v = np.empty((N, K // 2), np.uint8)
+    s = np.empty((N, K // 16), np.uint8)
+    g = C.c_float()
+    e = C.c_double()
+    _check(lib.lq_quantize_nvfp4(_np_ptr(w), N, K, _np_ptr(v), _np_ptr(s), C.byref(g), C.byref(e)))
+    return v, s, g.value, e.value
+
+
+def quantize_fp8_channel(w):
+    """[N][K] float32 / float16 / BF16 bits -> (q [N][K] E4M3, scale [N]) (drafter_variants.py:77-81)."""
+    import numpy as np
+    w, dt = _host_w(w)
+    N, K = w.shape
+    q = np.empty((N, K), np.uint8)
+    s = np.empty(N, np.float32)
+    _check(lib.lq_quantize_fp8_channel(_np_ptr(w), dt, N, K, _np_ptr(q), _np_ptr(s)))
+    return q, s
+
+
+def quantize_fp8_block128(w):
+    """[N][K] -> (q [N][K] E4M3, scale [ceil(N/128)][ceil(K/128)])."""
+    import numpy as np
+    w, dt = _host_w(w)
+    N, K = w.shape
+    q = np.empty((N, K), np.uint8)
+    s = np.empty(((N + 127) // 128, (K + 127) // 128), np.float32)
+    _check(lib.lq_quantize_fp8_block128(_np_ptr(w), dt, N, K, _np_ptr(q), _np_ptr(s)))
+    return q, s

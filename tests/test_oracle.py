@@ -350,3 +350,117 @@ def test_rmsnorm_quant_oracle_consistency():
     ref = x.astype(np.float64) / np.sqrt(np.mean(x.astype(np.float64) ** 2, axis=1, keepdims=True) + 1e-6)
     ref *= 1.0 + O.bf16_to_f32(w).astype(np.float64)
     assert np.max(np.abs(out - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+# ---------------- independent pins of the prefill checker and the fused SwiGLU quantizer ----------------
+def _e4m3_table() -> np.ndarray:
+    """E4M3 decode from torch's own float8_e4m3fn (an implementation independent of the oracle's)."""
+    return torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+
+
+def test_prefill_fp8_rows_vs_float64_block_product():
+    """or_prefill_fp8_rows (the block-scaled prefill checker; reference prefill_gemm.cu:269-342 and the check of
+    tests/prefill_tests.cu:179-207) against a float64 product written here from the definition: E4M3 decoded by
+    torch, the 1x128 activation scales repeated along K and the 128x128 weight scales repeated along N and K with
+    np.repeat. Scales span 2^-6 .. 2^6 so that a wrong scale index moves the result far outside the FP32 bound;
+    the same check applied to products with a transposed or shifted scale index fails."""
+    M, N, K = 40, 384, 512  # 3 x 4 weight blocks, 4 activation groups per row
+    rng = np.random.default_rng(77)
+    xq = rng.integers(0, 256, (M, K), dtype=np.uint8)
+    wq = rng.integers(0, 256, (N, K), dtype=np.uint8)
+    xq[(xq & 0x7F) == 0x7F] = 0x10  # no NaN codes
+    wq[(wq & 0x7F) == 0x7F] = 0x21
+    xs = np.exp2(rng.integers(-6, 7, (M, K // 128))).astype(np.float32) * rng.uniform(0.5, 1, (M, K // 128)).astype(np.float32)
+    ws = np.exp2(rng.integers(-6, 7, (N // 128, K // 128))).astype(np.float32) * rng.uniform(0.5, 1, (N // 128, K // 128)).astype(np.float32)
+    rows = np.array([0, 3, 17, 39], np.int32)
+    got = O.prefill_fp8_rows(xq, xs, rows, wq, ws).astype(np.float64)
+
+    e = _e4m3_table().astype(np.float64)
+
+    def ref(xs_full, ws_full):
+        xd = e[xq[rows]] * xs_full[rows]
+        wd = e[wq] * ws_full
+        return xd @ wd.T, np.abs(xd) @ np.abs(wd).T
+
+    xs_full = np.repeat(xs.astype(np.float64), 128, axis=1)
+    ws_full = np.repeat(np.repeat(ws.astype(np.float64), 128, axis=0), 128, axis=1)
+    want, mag = ref(xs_full, ws_full)
+    # FP32 accumulation of K exactly-rounded products: |err| <= K * 2^-24 * sum |terms| (a loose, safe bound)
+    bound = K * 2.0 ** -24 * mag + 1e-30
+    assert np.all(np.abs(got - want) <= bound)
+    # the check has teeth: a transposed weight-scale grid, or activation scales shifted by one group, fail it
+    xs_shift = np.repeat(np.roll(xs, 1, axis=1).astype(np.float64), 128, axis=1)
+    # ws[(n % 128) / 128] (always block row 0) and xs[m][k / 64] (clipped to the last group)
+    ws_row0 = np.repeat(np.repeat(ws[np.zeros(N // 128, int)].astype(np.float64), 128, axis=0), 128, axis=1)
+    xs_k64 = xs.astype(np.float64)[:, np.minimum(np.arange(K) // 64, K // 128 - 1)]
+    for bad_x, bad_w in ((xs_shift, ws_full), (xs_full, ws_row0), (xs_k64, ws_full)):
+        b, _ = ref(bad_x, bad_w)
+        assert not np.all(np.abs(got - b) <= bound)
+
+
+def _nvfp4_act_numpy(v: np.ndarray, g: float):
+    """The NVFP4 activation encoding written from its definition (reference prefill_gemm.cu:382-394): per block of
+    16, sc = E4M3_rne(g * amax / 6) (torch's cast, saturated at 448), os = 1 / (sc * (1 / g)) (0 if sc is 0), and
+    each code the E2M1 value nearest to v * os with ties to the even code, saturating at 6, sign kept."""
+    M, K = v.shape
+    b = v.reshape(M, K // 16, 16).astype(np.float32)
+    amax = np.abs(b).max(axis=2)
+    t = torch.from_numpy((np.float32(g) * (amax * np.float32(1.0 / 6.0))).astype(np.float32))
+    sc = t.clamp(max=448.0).to(torch.float8_e4m3fn)
+    sv = sc.float().numpy()
+    with np.errstate(divide="ignore"):
+        os_ = np.where(sv != 0, np.float32(1.0) / (sv * np.float32(1.0 / g)), np.float32(0)).astype(np.float32)
+    y = (b * os_[..., None]).astype(np.float32)
+    mag = np.abs(y).astype(np.float64)
+    grid = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float64)
+    dist = np.abs(mag[..., None] - grid)
+    best = dist.min(axis=-1, keepdims=True)
+    cand = dist == best
+    # among the nearest codes prefer the even one (ties to even)
+    even = np.arange(8) % 2 == 0
+    code = np.where((cand & even).any(-1), np.argmax(cand & even, axis=-1), np.argmax(cand, axis=-1))
+    code = np.where(mag >= 6, 7, code).astype(np.uint8)
+    code |= (np.signbit(y).astype(np.uint8) << 3)
+    c = code.reshape(M, K)
+    q = (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+    return q, sc.view(torch.uint8).numpy().reshape(M, K // 16)
+
+
+def test_quant_act_nvfp4_vs_independent_encoder():
+    x = O.bf16_to_f32(O.normal_bf16(21, 1.0, (6, 512)))
+    x[0, :16] = [6, -6, 3, 0.1, -0.1, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5, -5, 0, -0.0, 0.26]
+    for s in (1.0, 0.37):
+        q, sf = O.quant_act_nvfp4(x, s)
+        qn, sn = _nvfp4_act_numpy(x, 1.0 / s)
+        assert np.array_equal(sf, sn)
+        assert np.array_equal(q, qn)
+
+
+def test_silu_mul_quant_nvfp4_pinned():
+    """silu_mul_quant_nvfp4(g, u) (reference prefill_gemm.cu:404-420 with SILU, 613-618) is the NVFP4 encoding of
+    bf16(silu(g) * u): checked against the independent encoder on silu computed here in float64 and rounded to
+    FP32 (values whose FP32 silu differs by an ulp from expf's may round to another BF16: at most a few codes), and
+    against known answers: g = 0 gives a zero block (scale byte 0, codes 0); g = 20, u = 1.5 gives silu = 20
+    exactly in FP32, so a block of 30s has scale E4M3(5) and every code 7 (6.0)."""
+    g = O.normal_f32(31, 2.0, (8, 1024))
+    u = O.normal_f32(32, 1.0, (8, 1024))
+    q, sf = O.silu_mul_quant_nvfp4(g, u, 0.5)
+    g64 = g.astype(np.float64)
+    v = ((g64 / (1.0 + np.exp(-g64))).astype(np.float32) * u).astype(np.float32)
+    v = O.bf16_to_f32(O.f32_to_bf16(v))
+    qn, sn = _nvfp4_act_numpy(v, 2.0)
+    assert np.mean(sf != sn) <= 2e-3
+    assert np.mean(q != qn) <= 2e-3
+    # known answers
+    z = np.zeros((1, 16), np.float32)
+    q0, s0 = O.silu_mul_quant_nvfp4(z, np.full((1, 16), 3.0, np.float32), 1.0)
+    assert s0[0, 0] == 0 and np.all(q0 == 0)
+    big = np.full((1, 16), 20.0, np.float32)
+    q1, s1 = O.silu_mul_quant_nvfp4(big, np.full((1, 16), 1.5, np.float32), 1.0)
+    assert s1[0, 0] == torch.tensor([5.0]).to(torch.float8_e4m3fn).view(torch.uint8).item() == 0x4A
+    assert np.all(q1 == 0x77)
+    # large negative g: silu(g) * u is a tiny negative value whose block scale is E4M3 of it / 6
+    neg = np.full((1, 16), -30.0, np.float32)
+    q2, s2 = O.silu_mul_quant_nvfp4(neg, np.ones((1, 16), np.float32), 1.0)
+    t = O.bf16_to_f32(O.f32_to_bf16(np.array([-30.0 / (1.0 + np.exp(30.0))], np.float32)))[0]
+    assert s2[0, 0] == torch.tensor([abs(t) / 6.0]).to(torch.float8_e4m3fn).view(torch.uint8).item()

@@ -328,3 +328,91 @@ def test_hostile_headers_fail(tmp_path):
         f.write(struct.pack("<Q", 1 << 40) + b"{}")
     with pytest.raises(L.LingGemmError, match="bad header length"):
         LC.compile_checkpoint(d, out)
+
+
+def test_compile_quantizes_high_precision_linears(tmp_path):
+    """--quantize: BF16 / F32 linears become FP8 per-channel, FP8 block or NVFP4 entries equal to the library's
+    host quantizers (pinned against the oracle in test_quantize.py) followed by the retile; embeddings, norms and
+    untileable matrices are left to the passthrough."""
+    d = str(tmp_path / "hp")
+    wb = O.normal_bf16(41, 0.02, (64, 256))
+    wf = O.normal_f32(42, 0.02, (32, 384))
+    emb = O.normal_bf16(43, 0.02, (64, 256))
+    odd = O.normal_bf16(44, 0.02, (24, 256))  # N % 16 != 0
+    _single(d, {"m.q_proj.weight": ("BF16", wb.shape, wb), "m.o_proj.weight": ("F32", wf.shape, wf),
+                "m.o_proj.input_scale": ("F32", [], np.float32([0.5])),
+                "m.embed_tokens.weight": ("BF16", emb.shape, emb), "m.odd.weight": ("BF16", odd.shape, odd),
+                "m.post_norm.weight": ("BF16", (256,), wb[0])})
+    for mode in ("fp8", "fp8-block", "nvfp4"):
+        out = str(tmp_path / f"{mode}.lqw")
+        n = LC.compile_checkpoint(d, out, quantize=mode, passthrough=True)
+        assert n == 5
+        with LC.WeightFile(out) as f:
+            assert {f.entry(i).name for i in range(len(f))} == {"m.q_proj", "m.o_proj", "m.embed_tokens.weight",
+                                                                 "m.odd.weight", "m.post_norm.weight"}
+            for name, src, dt in (("m.q_proj", wb, "BF16"), ("m.o_proj", wf, "F32")):
+                e = f.entry(name)
+                f.verify(name)
+                assert e.quantized and e.dtype == dt
+                N, K = src.shape
+                if mode == "nvfp4":
+                    bf = src if dt == "BF16" else O.f32_to_bf16(src)
+                    v, s, g, _ = L.quantize_nvfp4(bf)
+                    assert np.float32(e.weight_scale) == np.float32(g)
+                    if e.kind == L.WENTRY_NVFP4_CODED:
+                        ok, table, code_of = L.scale_code_table(s)
+                        blob, raw = O.retile_nvfp4_coded(v, s, code_of)
+                        assert np.array_equal(e.blob, blob) and np.array_equal(e.aux, raw)
+                    else:
+                        assert np.array_equal(e.blob, O.retile_nvfp4(v, s))
+                else:
+                    q, s = (L.quantize_fp8_channel if mode == "fp8" else L.quantize_fp8_block128)(src)
+                    assert e.kind == L.WENTRY_FP8
+                    assert e.scale_kind == (L.WSCALE_CHANNEL if mode == "fp8" else L.WSCALE_BLOCK128)
+                    assert np.array_equal(e.blob, O.retile_fp8(q))
+                    assert np.array_equal(e.aux.view(np.float32), s.reshape(-1))
+            assert f.entry("m.o_proj").input_scale == 0.5
+            for raw in ("m.embed_tokens.weight", "m.odd.weight", "m.post_norm.weight"):
+                assert f.entry(raw).kind == L.WENTRY_RAW
+    with pytest.raises(L.LingGemmError, match="at most one"):
+        L._check(L.lib.lq_wfile_compile(d.encode(), str(tmp_path / "x.lqw").encode(),
+                                        L.WFILE_QUANT_FP8 | L.WFILE_QUANT_NVFP4, None))
+
+
+def _rehash_meta(b: bytearray) -> None:
+    """Recompute the entry-table hash after editing an entry, so that only the new bound checks can catch it."""
+    strings_off, strings_bytes = struct.unpack_from("<QQ", b, 24)
+    struct.pack_into("<Q", b, 56, _hash64(bytes(b[64:strings_off + strings_bytes])))
+
+
+def _hash64(data: bytes) -> int:
+    """FNV-1a over little-endian 64-bit words, the tail zero-padded, seeded with the byte count (the file's hash)."""
+    h = (0xcbf29ce484222325 ^ len(data)) & 0xFFFFFFFFFFFFFFFF
+    pad = data + b"\0" * (-len(data) % 8)
+    for (w,) in struct.iter_unpack("<Q", pad):
+        h ^= w
+        h = (h * 0x100000001b3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_hostile_entries_fail(compiled, tmp_path):
+    """Entries that pass the hash but lie about their sizes or names: a name offset that wraps, a blob shorter than
+    the tiled size of the entry's N and K, an aux table of the wrong size."""
+    out, _ = compiled
+    raw = bytearray(open(out, "rb").read())
+    _rehash_meta(raw)
+    assert bytes(raw) == open(out, "rb").read()  # the restated hash is the file's
+    bad = str(tmp_path / "hostile.lqw")
+    rec = 64  # entry 0
+    cases = [
+        (rec + 0, "<Q", 0xFFFFFFFFFFFFFFF0, "bad name"),          # name_off + name_len wraps
+        (rec + 104, "<Q", 4096, "section sizes"),                  # blob_bytes smaller than tiled_bytes(N, K)
+        (rec + 120, "<Q", 12, "section sizes|out of the file"),   # aux_bytes wrong for the kind
+    ]
+    for off, fmt, val, msg in cases:
+        b = bytearray(raw)
+        struct.pack_into(fmt, b, off, val)
+        _rehash_meta(b)
+        open(bad, "wb").write(bytes(b))
+        with pytest.raises(L.LingGemmError, match=msg):
+            LC.WeightFile(bad)
