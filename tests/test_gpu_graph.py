@@ -107,3 +107,39 @@ def test_block_prefill_under_graph_replay(L):
         run(ye)
         torch.cuda.synchronize()
         assert torch.equal(got, ye.view(torch.int16)), f"prefill replay {rep}"
+
+
+def test_prefill_scratch_is_not_reallocated(L):
+    """A graph captured over a tail-split prefill keeps its scratch pointers valid after a larger tail-split shape has
+    run eagerly (the library reserves the scratch at its bound once and never reallocates it)."""
+    M, N, K = 300, 256, 4096
+    qw, sw = O.quant_fp8_block128(O.normal_f32(131, 0.02, (N, K)))
+    tw, ws = L.retile_fp8(to_dev(qw)), to_dev(sw)
+    x = bf16(132, (M, K))
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+
+    def run(yy):
+        xq, xs = L.quant_act_fp8_g128(x)
+        L.prefill_fp8_block(xq, xs, tw, ws, N, y=yy)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run(y)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(y)
+    ref = torch.empty_like(y)
+    run(ref)
+    # a larger tail split: more rows and weight rows, so more split tiles than the captured shape
+    N2, M2 = 1024, 700
+    qw2, sw2 = O.quant_fp8_block128(O.normal_f32(133, 0.02, (N2, K)))
+    xq2, xs2 = L.quant_act_fp8_g128(bf16(134, (M2, K)))
+    L.prefill_fp8_block(xq2, xs2, L.retile_fp8(to_dev(qw2)), to_dev(sw2), N2)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {rep} after the larger shape"

@@ -268,6 +268,34 @@ def test_rmsnorm_quant(L, nvfp4):
     assert np.array_equal(q2.cpu().numpy(), q.cpu().numpy())
 
 
+@pytest.mark.parametrize("nvfp4", [False, True])
+def test_rmsnorm_quant_bf16(L, nvfp4):
+    """rmsnorm_quant_bf16 (reference prefill_gemm.cu:640-645): the same codes and scales as rmsnorm_quant, and a BF16
+    copy equal to the BF16 rounding of rmsnorm_quant's FP32 output."""
+    M, H = 7, 5120
+    x = O.normal_f32(43, 3.0, (M, H))
+    w = to_dev(O.normal_bf16(44, 0.2, (H,)).view(np.int16))
+    scale = 0.01 if nvfp4 else 0.02
+    out, q, sf = L.rmsnorm_quant(to_dev(x), w, 1e-6, nvfp4, scale)
+    ob, qb, sfb = L.rmsnorm_quant_bf16(to_dev(x), w, 1e-6, nvfp4, scale)
+    assert np.array_equal(qb.cpu().numpy(), q.cpu().numpy())
+    if nvfp4:
+        assert np.array_equal(sfb.cpu().numpy(), sf.cpu().numpy())
+    want = O.f32_to_bf16(out.cpu().numpy())
+    assert np.array_equal(ob.view(torch.int16).cpu().numpy().view(np.uint16), want)
+    _, q2, _ = L.rmsnorm_quant_bf16(to_dev(x), w, 1e-6, nvfp4, scale, with_out=False)
+    assert np.array_equal(q2.cpu().numpy(), q.cpu().numpy())
+
+
+def test_quant_act_fp8_bf16in_bit_exact(L):
+    """quant_act_fp8_bf16in (reference prefill_gemm.cu:626-630): the bytes quant_act_fp8 gives for the FP32 values
+    the BF16 copy holds."""
+    xb = O.f32_to_bf16(O.normal_f32(62, 3.0, (37, 512)))
+    xb[0, :4] = O.f32_to_bf16(np.array([0.0, -0.0, 1e6, -1e6], np.float32))
+    q = L.quant_act_fp8_bf16in(to_dev(xb.view(np.int16)).view(torch.bfloat16), 0.0123)
+    assert np.array_equal(q.cpu().numpy(), O.quant_act_fp8(O.bf16_to_f32(xb), 0.0123))
+
+
 def test_activation_producer_errors(L):
     x = torch.zeros((2, 24), dtype=torch.float32, device=DEV)
     with pytest.raises(L.LingGemmError, match="K % 16"):

@@ -216,15 +216,22 @@ def test_to_half_rows_bit_exact(L):
     assert np.array_equal(binv.cpu().numpy(), winv2)
 
 
-@pytest.mark.parametrize("K", [100, 1000, 3000, 8192, 12000, 32768])
+@pytest.mark.parametrize("K", [100, 1000, 3000, 8192, 12000, 32768, 40000, 65600])
 def test_to_half_rows_row_widths(L, K):
-    """Rows held in registers (up to 32768 values a row), including widths that leave a ragged tail."""
+    """Rows held in registers (up to 32768 values a row), including widths that leave a ragged tail, and longer rows
+    (the split-grid form: each block converts a slice), from FP32 and from BF16."""
     x = O.normal_f32(13 + K, 1.0, (5, K))
     x[4] = 0
+    x[2, K - 1] = 7.0e4  # the row's largest magnitude in the last slice
     xh, xinv = L.to_half_rows(to_dev(x))
     wh, winv = O.to_half_rows(x)
     assert np.array_equal(xh.view(torch.int16).cpu().numpy().view(np.uint16), wh)
     assert np.array_equal(xinv.cpu().numpy(), winv)
+    xb = O.f32_to_bf16(x)
+    bh, binv = L.bf16_to_half_rows(bf16_dev(xb))
+    wh2, winv2 = O.to_half_rows(O.bf16_to_f32(xb))
+    assert np.array_equal(bh.view(torch.int16).cpu().numpy().view(np.uint16), wh2)
+    assert np.array_equal(binv.cpu().numpy(), winv2)
 
 
 def reference_style_weights(seed, N, K):
