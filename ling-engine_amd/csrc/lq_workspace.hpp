@@ -33,5 +33,7 @@ struct Workspace {
 Workspace* workspace_for_current_device();
 // Reserves the prefill's tail-split scratch at its bound (one FP32 tile per CU, one counter per CU), once.
 int reserve_prefill_scratch(Workspace* ws);
+// Looks up the no-allocation entry point's scratch on the current device and clears its counters (synchronously).
+int noalloc_init_current_device();
 
 }  // namespace lq

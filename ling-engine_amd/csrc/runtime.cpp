@@ -177,6 +177,8 @@ int lq_init(void) {
   if (rc) return rc;
   rc = lq::reserve_prefill_scratch(ws);
   if (rc) return rc;
+  rc = lq::noalloc_init_current_device();
+  if (rc) return rc;
   return hipDeviceSynchronize() == hipSuccess ? LQ_OK : lq::fail(LQ_ERR_DEVICE, "lq_init: device synchronize failed");
 }
 

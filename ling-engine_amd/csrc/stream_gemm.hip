@@ -38,6 +38,7 @@
 #include <cstddef>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 #include <utility>
@@ -1402,18 +1403,37 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
   return LQ_OK;
 }
 
+// A fixed scratch region in place of the workspace (the no-allocation entry point): partials and counters, with
+// their capacities; the launch is rejected when it needs more.
+struct FixedScratch {
+  float* partials;
+  size_t partial_bytes;
+  int* counters;
+  size_t counter_count;
+};
+
 int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, const void* x, const float* xinv, int M,
-                  const Mat* mats, int n, int K, hipStream_t s) {
+                  const Mat* mats, int n, int K, hipStream_t s, const FixedScratch* fixed = nullptr) {
   StreamArgs a;
   int rc = stream_args(name, fmt, f16, pair, outf32, x, xinv, M, mats, n, K, a);
   if (rc) return rc;
-  Workspace* ws = workspace_for_current_device();
-  if (!ws) return LQ_ERR_DEVICE;
-  rc = ws->reserve_stream(2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float),
-                          static_cast<size_t>(a.TG));
-  if (rc) return rc;
-  a.partials = ws->partials;
-  a.counters = ws->counters;
+  const size_t pbytes = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float);
+  if (fixed) {
+    if (pbytes > fixed->partial_bytes || static_cast<size_t>(a.TG) > fixed->counter_count)
+      return fail(LQ_ERR_SHAPE, std::string(name) + ": the launch needs " + std::to_string(pbytes) +
+                                    " bytes of partial sums and " + std::to_string(a.TG) +
+                                    " counters; the fixed scratch holds " + std::to_string(fixed->partial_bytes) +
+                                    " and " + std::to_string(fixed->counter_count));
+    a.partials = fixed->partials;
+    a.counters = fixed->counters;
+  } else {
+    Workspace* ws = workspace_for_current_device();
+    if (!ws) return LQ_ERR_DEVICE;
+    rc = ws->reserve_stream(pbytes, static_cast<size_t>(a.TG));
+    if (rc) return rc;
+    a.partials = ws->partials;
+    a.counters = ws->counters;
+  }
 #ifdef LQ_STREAM_TRACE
   a.trace = g_trace;
 #endif
@@ -1506,7 +1526,65 @@ int half_rows(bool bf16in, const void* x, int M, int K, uint16_t* xh, float* xin
   return check_launch(nm);
 }
 
+__global__ void __launch_bounds__(256) zero_ints_kernel(int* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
 }  // namespace
+}  // namespace lq
+
+// ---------------- the no-allocation entry point's scratch ----------------
+// lq_stream_fp8_pc_noalloc keeps its split-K partial sums and arrival counters in this file-scope device array
+// instead of the library's workspace: 20 MiB of partials (two slots per workgroup at 256 workgroups, two tiles per
+// wave and five row groups: M <= 80) and 64 Ki counters. Every GPU the library runs on holds its own copy until the
+// process ends. Host code never passes the array's name to a kernel (on the host it is only a stand-in): its
+// device address is looked up once per device (noalloc_scratch) and that address is used.
+constexpr size_t kScratchPartialBytes = size_t(20) << 20;
+constexpr size_t kScratchCounters = size_t(1) << 16;
+static __device__ __align__(256) unsigned char scratch[kScratchPartialBytes + 4 * kScratchCounters];
+
+namespace lq {
+namespace {
+std::mutex g_scratch_mutex;
+constexpr int kScratchDevices = 64;
+unsigned char* g_scratch_ptr[kScratchDevices] = {};
+bool g_scratch_zeroed[kScratchDevices] = {};
+
+// The current device's scratch address (looked up on the first call per device), with its counters cleared once:
+// by lq_init (synchronously), or else by a fill kernel on `s` ahead of the first launch (captured into a graph if
+// the first call is captured). The counters are zero again at the end of every launch.
+int noalloc_scratch(hipStream_t s, bool sync, FixedScratch& fs) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices)
+    return fail(LQ_ERR_DEVICE, "stream_fp8_pc_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LQ_ERR_DEVICE, std::string("stream_fp8_pc_noalloc: scratch address lookup failed: ") +
+                                     hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+  }
+  fs.partials = reinterpret_cast<float*>(g_scratch_ptr[dev]);
+  fs.partial_bytes = kScratchPartialBytes;
+  fs.counters = reinterpret_cast<int*>(g_scratch_ptr[dev] + kScratchPartialBytes);
+  fs.counter_count = kScratchCounters;
+  if (!g_scratch_zeroed[dev]) {
+    hipLaunchKernelGGL(zero_ints_kernel, dim3(64), dim3(256), 0, s, fs.counters, static_cast<int>(kScratchCounters));
+    if (int rc = check_launch("stream_fp8_pc_noalloc")) return rc;
+    if (sync && hipStreamSynchronize(s) != hipSuccess)
+      return fail(LQ_ERR_DEVICE, "stream_fp8_pc_noalloc: clearing the scratch counters failed");
+    g_scratch_zeroed[dev] = true;
+  }
+  return LQ_OK;
+}
+}  // namespace
+
+int noalloc_init_current_device() {
+  FixedScratch fs;
+  return noalloc_scratch(nullptr, true, fs);
+}
 }  // namespace lq
 
 using namespace lq;
@@ -1585,6 +1663,17 @@ int lq_stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* ws
   const Mat m{w, nullptr, wscale_n, 0.f, y, nullptr, N, N};
   return stream_launch("stream_fp8_pc", kFp8, false, false, false, x, nullptr, M, &m, 1, K,
                        static_cast<hipStream_t>(stream));
+}
+
+int lq_stream_fp8_pc_noalloc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N,
+                             int K, void* stream) {
+  if (int rc = check_rows("stream_fp8_pc_noalloc", M, N, K)) return rc;
+  if (!wscale_n) return fail(LQ_ERR_ARG, "stream_fp8_pc_noalloc: null scales");
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  FixedScratch fs;
+  if (int rc = noalloc_scratch(s, false, fs)) return rc;
+  const Mat m{w, nullptr, wscale_n, 0.f, y, nullptr, N, N};
+  return stream_launch("stream_fp8_pc_noalloc", kFp8, false, false, false, x, nullptr, M, &m, 1, K, s, &fs);
 }
 
 int lq_stream_fp8_pc_silu_mul(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate,

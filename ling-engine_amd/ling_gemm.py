@@ -41,6 +41,7 @@ SIGNATURES = {
     "lq_stream_gemm_multi": (_I, [_I, _P, _P, _I, _P, _I, _I, _P]),
     "lq_stream_gemm_gather_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _P, _I, _P, _I, _I, _P]),
     "lq_stream_fp8_pc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
+    "lq_stream_fp8_pc_noalloc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_residual": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_ffn": (_I, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P]),
@@ -339,6 +340,15 @@ def stream_fp8_pc(x, w, wscale_n, N: int, y=None):
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if y is None else y
     _check(lib.lq_stream_fp8_pc(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(_dev(wscale_n, torch.float32)),
                                 _ptr(y), N, K, _stream()))
+    return y
+
+
+def stream_fp8_pc_noalloc(x, w, wscale_n, N: int, y=None):
+    """stream_fp8_pc with the library's fixed scratch instead of its workspace (allocates nothing; y is the caller's)."""
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x.device) if y is None else y
+    _check(lib.lq_stream_fp8_pc_noalloc(_ptr(_dev(x, torch.bfloat16)), M, _ptr(w), _ptr(wscale_n), _ptr(y), N, K,
+                                        _stream()))
     return y
 
 
