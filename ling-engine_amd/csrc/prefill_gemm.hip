@@ -72,11 +72,13 @@ enum PrefillOut { kOutBf16 = 0, kOutF32 = 1, kOutF32Acc = 2 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// soff is uniform over the wave; saying so keeps it in an SGPR (held in a VGPR, the compiler wraps every load in a
+// loop over the lanes' distinct values).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 16, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 4, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 4, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 // s_waitcnt with only vmcnt / lgkmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8])
 #define LQ_WAIT_VM0() __builtin_amdgcn_s_waitcnt(0x0f70)

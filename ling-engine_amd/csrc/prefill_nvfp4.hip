@@ -60,11 +60,13 @@ struct Nvfp4Args {
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
+// soff is uniform over the wave; saying so keeps it in an SGPR (held in a VGPR, the compiler wraps every load in a
+// loop over the lanes' distinct values).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 16, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 16, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 __device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t rs, uint8_t* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 4, voff, soff, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds), 4, voff, __builtin_amdgcn_readfirstlane(soff), 0, 0);
 }
 
 // Step s of a lane's raw chunk (word d = 8 E2M1 codes of its 16 bytes, two E4M3 scale bytes): 8 FP16 values
