@@ -112,7 +112,9 @@ typedef struct {
   float* y;
   int N;
 } lq_stream_target;
-/* 1..4 matrices sharing xh in one launch, each y = scale * xh . W^T * xinv. kernels.cuh:288-289 stream_gemm_multi */
+/* 1..4 matrices sharing xh in one launch, each y = scale * xh . W^T * xinv, bit for bit what a separate call for that
+ * matrix gives (each matrix's K is split over its own workgroups as it would be alone; matrices wanting different
+ * tiles per wave, or mixing coded and raw NVFP4, take one launch per group). kernels.cuh:288-289 stream_gemm_multi */
 int lq_stream_gemm_multi(int nvfp4, const uint16_t* xh, const float* xinv, int M, const lq_stream_target* t, int n,
                          int K, void* stream);
 

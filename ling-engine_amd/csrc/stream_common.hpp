@@ -39,9 +39,8 @@ struct StreamArgs {
   const void* x;      // [M][K] BF16 or FP16
   const float* xinv;  // [M] row scales of an FP16 copy, or null
   int M, K, C;        // C = K / 128
-  int P;              // logical workgroups
-  int U;              // units = TG * C (U * (P + 1) < 2^31: the unit arithmetic is 32-bit)
-  int TG;             // tile groups
+  int P;              // logical workgroups (all segments)
+  int TG;             // tile groups (all segments)
   int T;              // tiles per wave (the kernel's template argument)
   int count;          // matrices
   const uint8_t* w[kMaxMats];
@@ -52,6 +51,11 @@ struct StreamArgs {
   const uint16_t* resid[kMaxMats];  // BF16 residual [M][ldy] or null
   int N[kMaxMats];
   int tg0[kMaxMats + 1];  // first tile group of each matrix; tg0[count] = TG
+  // Segments: each matrix of a launch that is not a SiLU*mul pair (a pair is one segment) has its tile groups
+  // [tg0[i], tg0[i + 1]) split over its own workgroups [wg0[i], wg0[i + 1]), exactly as a launch of that matrix
+  // alone splits them, so a matrix's results do not depend on the matrices beside it. Units (tile group, chunk) of
+  // a segment: U = (tg0[i + 1] - tg0[i]) C, with U (P + 1) < 2^31 (the unit arithmetic is 32-bit).
+  int wg0[kMaxMats + 1];
   int ldy[kMaxMats];
   float* partials;  // [2 * P][T * G * 4][256] per workgroup slot
   int* counters;    // [TG]
@@ -59,7 +63,7 @@ struct StreamArgs {
 };
 
 // The kernel touches one field per 64-byte line of its arguments at entry (see stream_kernel).
-static_assert(sizeof(StreamArgs) <= 320 && offsetof(StreamArgs, x) / 64 == 0 &&
+static_assert(sizeof(StreamArgs) <= 320 && offsetof(StreamArgs, trace) < 320 && offsetof(StreamArgs, x) / 64 == 0 &&
                   (offsetof(StreamArgs, w) + 2 * sizeof(void*)) / 64 == 1 &&
                   (offsetof(StreamArgs, svec) + 2 * sizeof(void*)) / 64 == 2 && offsetof(StreamArgs, resid) / 64 == 3 &&
                   (offsetof(StreamArgs, tg0) + 4 * sizeof(int)) / 64 == 4,
@@ -72,7 +76,7 @@ template <int N, class X>
 __device__ __forceinline__ X pick(const X (&arr)[N], int mi) {
   X v = arr[0];
 #pragma unroll
-  for (int k = 1; k < kMaxMats; ++k) v = mi == k ? arr[k] : v;
+  for (int k = 1; k < N; ++k) v = mi == k ? arr[k] : v;
   return v;
 }
 
@@ -301,6 +305,40 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
 __device__ __forceinline__ int wg_of_unit(int u, int P, int U) { return ((u + 1) * P - 1) / U; }
 __device__ __forceinline__ int unit_start(int p, int P, int U) { return p * U / P; }
 
+// A segment's first tile group and workgroup, its workgroups P and its units U (see StreamArgs::wg0).
+struct SegSplit {
+  int tgb, wgb, P, U;
+};
+template <bool PAIR>
+__device__ __forceinline__ SegSplit seg_split(const StreamArgs& a, int i) {
+  SegSplit s;
+  s.tgb = PAIR ? 0 : pick(a.tg0, i);
+  const int tge = PAIR ? a.TG : pick(a.tg0, i + 1);
+  s.wgb = pick(a.wg0, i);
+  s.P = pick(a.wg0, i + 1) - s.wgb;
+  s.U = (tge - s.tgb) * a.C;
+  return s;
+}
+// The segment holding workgroup b (raw or logical: the permutation stays inside a segment), or tile group tg.
+template <bool PAIR>
+__device__ __forceinline__ int seg_of_wg(const StreamArgs& a, int b) {
+  int i = 0;
+  if constexpr (!PAIR) {
+#pragma unroll
+    for (int k = 1; k < kMaxMats; ++k) i += (k < a.count && b >= a.wg0[k]) ? 1 : 0;
+  }
+  return i;
+}
+template <bool PAIR>
+__device__ __forceinline__ int seg_of_tg(const StreamArgs& a, int tg) {
+  int i = 0;
+  if constexpr (!PAIR) {
+#pragma unroll
+    for (int k = 1; k < kMaxMats; ++k) i += (k < a.count && tg >= a.tg0[k]) ? 1 : 0;
+  }
+  return i;
+}
+
 // Tiles of tile group tg that this wave streams: PAIR = gate tile wtile0 then the same up tile; else tiles
 // wtile0 .. of matrix mi.
 template <int WF, int T, bool PAIR>
@@ -351,11 +389,14 @@ struct SplitInfo {
   int pf, pl;
   bool pf_first;
 };
+template <bool PAIR>
 __device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
+  const SegSplit g = seg_split<PAIR>(a, seg_of_tg<PAIR>(a, tg));
+  const int u = (tg - g.tgb) * a.C;
   SplitInfo s;
-  s.pf = wg_of_unit(tg * a.C, a.P, a.U);
-  s.pl = wg_of_unit(tg * a.C + a.C - 1, a.P, a.U);
-  s.pf_first = unit_start(s.pf, a.P, a.U) == tg * a.C;
+  s.pf = g.wgb + wg_of_unit(u, g.P, g.U);
+  s.pl = g.wgb + wg_of_unit(u + a.C - 1, g.P, g.U);
+  s.pf_first = unit_start(s.pf - g.wgb, g.P, g.U) == u;
   return s;
 }
 
@@ -486,10 +527,14 @@ struct NoWait {
 
 // Logical workgroup id: blockIdx.x % 8 is the XCD the hardware places it on; consecutive logical ids share an
 // XCD, so a tile group's partials are exchanged within one L2.
-__device__ __forceinline__ int logical_wg(int P) {
-  int p = blockIdx.x;
-  if ((P & 7) == 0) p = (blockIdx.x & 7) * (P >> 3) + (blockIdx.x >> 3);
-  return p;
+template <bool PAIR>
+__device__ __forceinline__ int logical_wg(const StreamArgs& a) {
+  const int b = blockIdx.x;
+  const SegSplit g = seg_split<PAIR>(a, seg_of_wg<PAIR>(a, b));
+  const int bl = b - g.wgb;
+  int p = bl;
+  if ((g.P & 7) == 0 && (g.wgb & 7) == 0) p = (bl & 7) * (g.P >> 3) + (bl >> 3);
+  return g.wgb + p;
 }
 
 }  // namespace lq

@@ -83,7 +83,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     __syncthreads();
   }
 
-  const int u0 = unit_start(p, a.P, a.U), u1 = unit_start(p + 1, a.P, a.U);
+  // this workgroup's units, in the global (tile group, chunk) numbering
+  const SegSplit seg = seg_split<PAIR>(a, seg_of_wg<PAIR>(a, p));
+  const int u0 = seg.tgb * a.C + unit_start(p - seg.wgb, seg.P, seg.U);
+  const int u1 = seg.tgb * a.C + unit_start(p - seg.wgb + 1, seg.P, seg.U);
   const int n_it = u1 - u0;  // chunks this workgroup streams
   if (n_it <= 0) {
     flush_trace(p);
@@ -353,7 +356,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   LQ_TS(3);
-  const SplitInfo si[2] = {split_info(a, tg_first), split_info(a, tg_last)};
+  const SplitInfo si[2] = {split_info<PAIR>(a, tg_first), split_info<PAIR>(a, tg_last)};
   // (selects rather than indexing si by thread: a thread-indexed local array would be placed in LDS)
   if (threadIdx.x < 2) {
     const bool h = threadIdx.x != 0;
@@ -398,7 +401,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
-  stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg(a.P), sm, NoWait{});
+  stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg<PAIR>(a), sm, NoWait{});
 }
 
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
@@ -414,7 +417,7 @@ constexpr unsigned long long kFfnDeadlineTicks = 10'000'000ull;  // s_memrealtim
 template <int G>
 __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const StreamArgs b, int* sync) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
-  const int p = logical_wg(a.P);
+  const int p = logical_wg<true>(a);  // (both phases are one segment of the same P workgroups)
   stream_body<G, kFp8, 2, false, true, false, kYCoh>(a, p, sm, NoWait{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores have completed
   __syncthreads();
@@ -847,32 +850,48 @@ unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the
 // FP32 floats of one partial slot (one workgroup's T x G accumulator vectors for 256 threads).
 size_t slot_floats(int T, int M) { return static_cast<size_t>(T) * cdiv(M, 16) * 4 * kThreads; }
 
-// Tiles per wave and the split for these matrices (sets a.T, a.TG, a.P, a.U). One FP8 tile per wave when a
-// workgroup's range would be short (under 10 chunks at two tiles) and a tile group would span more than 4
-// workgroups: there the finish dominates, and one tile per wave halves its fan-in and partial size. Depends on
-// the matrices' N, K and the device only, never on M (row invariance).
-int choose_tiles(const char* name, int fmt, bool pair, const int* Ns, int n, StreamArgs& a) {
-  auto split = [&](int T, long long& tg, long long& units, int& P) {
-    tg = 0;
-    if (pair) tg = cdiv(Ns[0], group_rows(T, true));
-    else
-      for (int i = 0; i < n; ++i) tg += cdiv(Ns[i], group_rows(T, false));
-    units = tg * a.C;
-    P = choose_wgs(units);
+// Tiles per wave, tile groups and workgroups of one matrix (or one SiLU*mul pair) launched alone. One FP8 tile per
+// wave when a workgroup's range would be short (under 10 chunks at two tiles) and a tile group would span more than
+// 4 workgroups: there the finish dominates, and one tile per wave halves its fan-in and partial size. Depends on the
+// matrix's N, K and the device only, never on M (row invariance).
+void matrix_split(int fmt, bool pair, int N, int C, int& T, int& tg, int& P) {
+  T = tiles_per_wave(fmt, pair);
+  auto go = [&]() {
+    tg = cdiv(N, group_rows(T, pair));
+    P = choose_wgs(static_cast<long long>(tg) * C);
   };
-  int T = tiles_per_wave(fmt, pair);
-  long long tg, units;
-  int P;
-  split(T, tg, units, P);
-  if (fmt == kFp8 && !pair && units < 10LL * P && P > 4 * tg) {
+  go();
+  if (fmt == kFp8 && !pair && static_cast<long long>(tg) * C < 10LL * P && P > 4 * tg) {
     T = 1;
-    split(T, tg, units, P);
+    go();
   }
-  if (units * (P + 1) >= (1LL << 31)) return fail(LQ_ERR_SHAPE, std::string(name) + ": matrices too large for one launch");
-  a.T = T;
-  a.TG = static_cast<int>(tg);
-  a.P = P;
-  a.U = static_cast<int>(units);
+}
+
+// The segments of a launch (sets a.T, a.TG, a.P, tg0, wg0): each matrix (a pair: both) split as it would be alone,
+// its workgroups after the previous matrix's. Returns kMixedTiles (nothing set) when the matrices want different
+// tiles per wave: the caller then launches them in groups.
+constexpr int kMixedTiles = -1;  // (distinct from every LQ_ERR_* status)
+int choose_tiles(const char* name, int fmt, bool pair, const int* Ns, int n, StreamArgs& a) {
+  const int nseg = pair ? 1 : n;
+  int T0 = -1, tgs = 0, wgs = 0;
+  for (int i = 0; i < nseg; ++i) {
+    int T, tg, P;
+    matrix_split(fmt, pair, Ns[i], a.C, T, tg, P);
+    if (T0 >= 0 && T != T0) return kMixedTiles;
+    T0 = T;
+    if (static_cast<long long>(tg) * a.C * (P + 1) >= (1LL << 31) || tgs + static_cast<long long>(tg) >= (1LL << 30))
+      return fail(LQ_ERR_SHAPE, std::string(name) + ": matrices too large for one launch");
+    a.tg0[i] = tgs;
+    a.wg0[i] = wgs;
+    tgs += tg;
+    wgs += P;
+  }
+  if (pair) a.tg0[1] = 0;
+  a.tg0[pair ? 2 : n] = tgs;
+  a.wg0[nseg] = wgs;
+  a.T = T0;
+  a.TG = tgs;
+  a.P = wgs;
   return LQ_OK;
 }
 
@@ -913,15 +932,8 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
     Ns[i] = m.N;
   }
   if (pair && (n != 2 || mats[0].N != mats[1].N)) return fail(LQ_ERR_SHAPE, nm + ": gate and up must have the same N");
-  if (int rc = choose_tiles(name, fmt, pair, Ns, n, a)) return rc;
-  int tg = 0;
-  for (int i = 0; i < n; ++i) {
-    a.tg0[i] = tg;
-    if (!pair) tg += cdiv(Ns[i], group_rows(a.T, false));
-  }
-  a.tg0[n] = a.TG;
   if (!pair && fmt != kFp8 && !f16 && outf32) return fail(LQ_ERR_ARG, nm + ": BF16 activations with NVFP4 give BF16 out");
-  return LQ_OK;
+  return choose_tiles(name, fmt, pair, Ns, n, a);  // (kMixedTiles: the matrices want different tiles per wave)
 }
 
 // A fixed scratch region in place of the workspace (the no-allocation entry point): partials and counters, with
@@ -937,6 +949,20 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
                   const Mat* mats, int n, int K, hipStream_t s, const FixedScratch* fixed = nullptr) {
   StreamArgs a;
   int rc = stream_args(name, fmt, f16, pair, outf32, x, xinv, M, mats, n, K, a);
+  if (rc == kMixedTiles) {
+    // matrices that want different tiles per wave: one launch per group of equal T, each matrix split as alone
+    for (int T : {1, 2, 4}) {
+      Mat sub[kMaxMats];
+      int k = 0;
+      for (int i = 0; i < n; ++i) {
+        int Ti, tg, P;
+        matrix_split(fmt, false, mats[i].N, K / kChunk, Ti, tg, P);
+        if (Ti == T) sub[k++] = mats[i];
+      }
+      if (k && (rc = stream_launch(name, fmt, f16, pair, outf32, x, xinv, M, sub, k, K, s, fixed))) return rc;
+    }
+    return LQ_OK;
+  }
   if (rc) return rc;
   const size_t pbytes = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float);
   if (fixed) {
@@ -1249,13 +1275,12 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.cap = cap;
   a.N = N;
   a.y = y;
-  // the full launch's split (choose_tiles for this N, K): its tiles per wave, tile groups, workgroups and units
-  StreamArgs full{};
-  full.C = a.C;
-  if (int rc = choose_tiles(nm.c_str(), kFp4, false, &N, 1, full)) return rc;
-  a.TGR = group_rows(full.T, false);
-  a.P = full.P;
-  a.U = full.U;
+  // the full launch's split (the matrix alone): its tiles per wave, tile groups, workgroups and units
+  int fT, ftg, fP;
+  matrix_split(kFp4, false, N, a.C, fT, ftg, fP);
+  a.TGR = group_rows(fT, false);
+  a.P = fP;
+  a.U = ftg * a.C;
   const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cdiv(M, 16)) {

@@ -418,3 +418,34 @@ def test_full_size_one_tile_shapes(L, N, K):
         got = bf16_host(L.stream_fp8_pc(xd[:M].contiguous(), tw, sd, N))
         assert_close_bf16(got, O.stream_fp8_pc_bf16(x[:M], q, s), f"M={M} N={N} K={K}")
         assert np.array_equal(got, full[:M]), f"row invariance M={M} N={N} K={K}"
+
+
+@pytest.mark.parametrize("K", [5120, 1024])
+def test_multi_is_bit_identical_to_separate_launches(L, K):
+    """stream_gemm_multi equals separate calls bit for bit (reference src/core/kernels.cuh:278-280), with matrices of
+    different N in one launch: each matrix is split over its own workgroups as it would be alone (q|k|v-like shapes;
+    at K = 1024 the short ranges give the FP8 matrices one tile per wave while the NVFP4 ones keep four, and the wide
+    one two). FP8 and NVFP4 (raw and coded), M = 17 and 68."""
+    x = O.normal_f32(70 + K, 1.0, (68, K))
+    for M in (17, 68):
+        xh, xinv = L.to_half_rows(to_dev(x[:M]))
+        fp8 = []
+        for i, N in enumerate((5120, 1024, 1024, 12352)):
+            q, _ = fp8_weights(80 + i + K, N, K)
+            fp8.append((L.retile_fp8(to_dev(q)), 0.25 + i, N))
+        sep = [L.stream_gemm_fp8(xh, xinv, w, sc, N, K).view(torch.int32).cpu().numpy() for w, sc, N in fp8]
+        ys = [torch.empty((M, N), dtype=torch.float32, device=DEV) for _, _, N in fp8]
+        L.stream_gemm_multi(False, xh, xinv, [(w, None, sc, y, N) for (w, sc, N), y in zip(fp8, ys)], K)
+        for i, y in enumerate(ys):
+            assert np.array_equal(y.view(torch.int32).cpu().numpy(), sep[i]), f"fp8 multi M={M} matrix {i}"
+        f4 = []
+        for i, N in enumerate((2048, 512, 6144)):
+            v, s, g, _ = O.quant_nvfp4(O.normal_bf16(90 + i + K, 0.02, (N, K)))
+            ok, table, code_of = O.scale_code_table(s)
+            blob, _ = L.retile_nvfp4_coded(to_dev(v), to_dev(s), to_dev(code_of))
+            f4.append((blob, to_dev(table), g, N) if ok and i == 1 else (L.retile_nvfp4(to_dev(v), to_dev(s)), None, g, N))
+        sep4 = [L.stream_gemm_nvfp4(xh, xinv, w, tab, g, N, K).view(torch.int32).cpu().numpy() for w, tab, g, N in f4]
+        ys = [torch.empty((M, N), dtype=torch.float32, device=DEV) for _, _, _, N in f4]
+        L.stream_gemm_multi(True, xh, xinv, [(w, tab, g, y, N) for (w, tab, g, N), y in zip(f4, ys)], K)
+        for i, y in enumerate(ys):
+            assert np.array_equal(y.view(torch.int32).cpu().numpy(), sep4[i]), f"nvfp4 multi M={M} matrix {i}"
