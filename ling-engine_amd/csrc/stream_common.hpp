@@ -41,7 +41,8 @@ struct StreamArgs {
   int M, K, C;        // C = K / 128
   int P;              // logical workgroups (all segments)
   int TG;             // tile groups (all segments)
-  int T;              // tiles per wave (the kernel's template argument)
+  short T;            // tiles per wave (the kernel's template argument)
+  short NR;           // finish workgroups per split tile group (0: the last workgroup to arrive finishes it)
   int count;          // matrices
   const uint8_t* w[kMaxMats];
   const uint8_t* table[kMaxMats];   // coded NVFP4: device scale-code table [64]
@@ -472,6 +473,178 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
     for (int g = 0; g < G; ++g)
       if (16 * g + r < a.M)
         __builtin_amdgcn_raw_buffer_store_b128(acc[i][g], prs, off + (i * G + g) * 16 * kThreads, 0, kSc1);
+}
+
+// Finish workgroups (StreamArgs::NR > 0, for launches whose tile groups each span several workgroups): launch
+// workgroup P + f finishes share f % NR of split tile group f / NR, the accumulator vectors that streaming wave
+// f % NR holds (NR = 4). The streaming workgroups publish their partials as in the last-arriver form, count
+// themselves on counters[tg] (an atomic whose result nobody waits for) and exit; each finish workgroup waits
+// for the full count, adds its share's partials in workgroup order and runs the epilogue on it, element for
+// element the last-arriver form's arithmetic. Four workgroups on four CUs read what one finisher read, and no
+// streaming workgroup spends its tail finishing two tile groups in a row. When all NR finish workgroups of tg
+// have seen the full count (counters[TG + tg] counts them), the last one clears both counters for the next
+// launch. A finish workgroup never holds up a streaming one: the dispatcher places workgroups in index order, so
+// every streaming workgroup has its CU before any finish workgroup starts waiting. The wait gives up after a
+// second (s_memrealtime at 100 MHz), which a launch whose streaming workgroups run never reaches.
+constexpr int kFinishShares = 4;
+constexpr unsigned long long kFinishWaitTicks = 100'000'000ull;
+
+template <int G, int T, bool PAIR, bool OUTF32>
+__device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
+  const int tg = f / kFinishShares, share = f % kFinishShares;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  unsigned long long ts[16] = {};
+  LQ_TS(0);
+#ifdef LQ_STREAM_TRACE
+  struct Flush {
+    const StreamArgs& a;
+    int f;
+    unsigned long long (&ts)[16];
+    __device__ ~Flush() {
+      LQ_TS(6);
+      if (a.trace && threadIdx.x == 0)
+        for (int k = 0; k < 16; ++k) a.trace[(a.P + f) * 16 + k] = ts[k];
+    }
+  } flush{a, f, ts};
+#else
+  (void)ts;
+#endif
+  const int r = lane & 15, t = lane >> 4;
+  if (tg >= a.TG) return;
+  const SplitInfo si = split_info<PAIR>(a, tg);
+  if (si.pf == si.pl) return;  // streamed whole by one workgroup, which finished it
+  const int n = si.pl - si.pf + 1;
+  const int mi = seg_of_tg<PAIR>(a, tg);
+  const int wtile0 = (tg - pick(a.tg0, mi)) * (group_rows(T, PAIR) / 16) + share * (PAIR ? T / 2 : T);
+  // units of the share: (tile, group) vectors, a SiLU*mul pair's gate and up vector together; wave w takes
+  // units w, w + 4, ...
+  constexpr int NU = (PAIR ? T / 2 : T) * G;
+  constexpr int UW = (NU + 3) / 4;
+  constexpr int SLOT = T * G * 16 * kThreads;  // bytes of one workgroup slot
+  const int vtid = share * 64 + lane;          // the streaming thread whose vectors these are
+  const int Nm = PAIR ? a.N[0] : pick(a.N, mi);
+  const float* const svec = PAIR ? nullptr : pick(a.svec, mi);
+  const uint16_t* const resid = PAIR ? nullptr : pick(a.resid, mi);
+  const int ldy = PAIR ? a.ldy[0] : pick(a.ldy, mi);
+
+  // epilogue inputs first (they do not depend on the partials)
+  f32x4 sv[UW][2];
+  u32x2 rr[UW];
+  float xi[UW];
+#pragma unroll
+  for (int k = 0; k < UW; ++k) {
+    const int u = wave + 4 * k;
+    const int i = u / G, g = u % G, tok = 16 * g + r;
+    const int col = (wtile0 + i) * 16 + 4 * t;
+    rr[k] = u32x2{0u, 0u};
+    xi[k] = 1.0f;
+    if constexpr (PAIR) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float sc = a.sc[h];
+        sv[k][h] = f32x4{sc, sc, sc, sc};
+        if (u < NU && a.svec[h] && col < Nm) sv[k][h] = *reinterpret_cast<const f32x4*>(a.svec[h] + col);
+      }
+    } else {
+      const float sc = pick(a.sc, mi);
+      sv[k][0] = f32x4{sc, sc, sc, sc};
+      if (u < NU && svec && col < Nm) sv[k][0] = *reinterpret_cast<const f32x4*>(svec + col);
+      if constexpr (!OUTF32)
+        if (u < NU && resid && tok < a.M && col < Nm)
+          rr[k] = *reinterpret_cast<const u32x2*>(resid + static_cast<size_t>(tok) * ldy + col);
+      if (u < NU && a.xinv && tok < a.M) xi[k] = a.xinv[tok];
+    }
+  }
+
+  // every streaming workgroup of tg has published and counted itself (one wave polls, about every half
+  // microsecond: the polls of all finish workgroups land on a few cache lines)
+  if (wave == 0) {
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT)) < n) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kFinishWaitTicks) break;
+      __builtin_amdgcn_s_sleep(16);
+    }
+  }
+  __syncthreads();
+  LQ_TS(1);
+  if (threadIdx.x == 0) {
+    const int old = __hip_atomic_fetch_add(a.counters + a.TG + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == kFinishShares - 1) {
+      __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.counters + a.TG + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+
+  const __amdgpu_buffer_rsrc_t prs = make_rsrc(a.partials);
+  constexpr int NH = PAIR ? 2 : 1;
+  constexpr int B = 8;  // partials per batch of loads
+#pragma unroll
+  for (int k = 0; k < UW; ++k) {
+    const int u = wave + 4 * k;
+    if (u >= NU) break;  // (uniform over the wave)
+    const int i = u / G, g = u % G, tok = 16 * g + r;
+    const unsigned rowmask = tok < a.M ? 0u : 0x80000000u;
+    f32x4 acc[NH];
+    for (int q0 = 0; q0 < n; q0 += B) {
+      f32x4 ring[B][NH];
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int q = si.pf + q0 + b;
+        const int which = (q0 + b == 0 && !si.pf_first) ? 1 : 0;
+        const unsigned oob = (q0 + b < n ? 0u : 0x80000000u) | rowmask;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          const int j = (i + h * (T / 2)) * G + g;
+          ring[b][h] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         prs, static_cast<int>(((2 * q + which) * SLOT + vtid * 16 + j * 16 * kThreads) | oob), 0,
+                         kSc1));
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+        if (q0 + b < n)
+#pragma unroll
+          for (int h = 0; h < NH; ++h) acc[h] = q0 + b == 0 ? ring[b][h] : acc[h] + ring[b][h];
+    }
+    if (k == 0) LQ_TS(2);
+    const int col = (wtile0 + i) * 16 + 4 * t;
+    if (tok >= a.M || col >= Nm) continue;
+    if constexpr (PAIR) {
+      uint16_t o[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float gs = acc[0][v] * sv[k][0][v];
+        const float us = acc[NH - 1][v] * sv[k][NH - 1][v];
+        o[v] = f32_to_bf16(silu(gs) * us);
+      }
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(a.y[0]) + static_cast<size_t>(tok) * ldy + col) =
+          u32x2{o[0] | (uint32_t(o[1]) << 16), o[2] | (uint32_t(o[3]) << 16)};
+    } else {
+      float vv[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        vv[v] = acc[0][v] * sv[k][0][v];
+        if (a.xinv) vv[v] = vv[v] * xi[k];
+      }
+      void* const y = pick(a.y, mi);
+      const size_t o = static_cast<size_t>(tok) * ldy + col;
+      if constexpr (OUTF32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(y) + o) = f32x4{vv[0], vv[1], vv[2], vv[3]};
+      } else {
+        if (resid) {
+          vv[0] = vv[0] + bf16_to_f32(rr[k].x & 0xffff);
+          vv[1] = vv[1] + bf16_to_f32(rr[k].x >> 16);
+          vv[2] = vv[2] + bf16_to_f32(rr[k].y & 0xffff);
+          vv[3] = vv[3] + bf16_to_f32(rr[k].y >> 16);
+        }
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(y) + o) =
+            u32x2{f32_to_bf16(vv[0]) | (uint32_t(f32_to_bf16(vv[1])) << 16),
+                  f32_to_bf16(vv[2]) | (uint32_t(f32_to_bf16(vv[3])) << 16)};
+      }
+    }
+  }
 }
 
 // G <= 2: a chunk's activation operands (all four steps) are read from LDS one chunk ahead, into registers,

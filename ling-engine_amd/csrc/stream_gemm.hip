@@ -356,6 +356,14 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   LQ_TS(3);
+  if (a.NR) {  // the finish workgroups add the partials
+    if (threadIdx.x == 0) {
+      if (splitF) __hip_atomic_fetch_add(a.counters + tg_first, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (splitL) __hip_atomic_fetch_add(a.counters + tg_last, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    flush_trace(p);
+    return;
+  }
   const SplitInfo si[2] = {split_info<PAIR>(a, tg_first), split_info<PAIR>(a, tg_last)};
   // (selects rather than indexing si by thread: a thread-indexed local array would be placed in LDS)
   if (threadIdx.x < 2) {
@@ -373,6 +381,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   __syncthreads();
   const bool doit[2] = {last_flag[0] != 0, last_flag[1] != 0};
   LQ_TS(4);
+#ifdef LQ_STREAM_TRACE
+  ts[15] = (doit[0] ? 1 : 0) + (doit[1] ? 2 : 0) + 4 * (si[0].pl - si[0].pf + 1) + 256 * (si[1].pl - si[1].pf + 1);
+#endif
   if (!doit[0] && !doit[1]) {
     flush_trace(p);
     return;
@@ -401,6 +412,10 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
+  if (static_cast<int>(blockIdx.x) >= a.P) {
+    finish_share<G, TW, PAIR, OUTF32>(a, static_cast<int>(blockIdx.x) - a.P);
+    return;
+  }
   stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg<PAIR>(a), sm, NoWait{});
 }
 
@@ -817,7 +832,8 @@ int choose_wgs(long long U) {
 
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g(const StreamArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), dim3(a.P), dim3(kThreads), 0, s, a);
+  hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), dim3(a.P + a.NR * a.TG), dim3(kThreads), 0,
+                     s, a);
   return check_launch("stream_gemm");
 }
 
@@ -936,6 +952,17 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
   return choose_tiles(name, fmt, pair, Ns, n, a);  // (kMixedTiles: the matrices want different tiles per wave)
 }
 
+// Finish workgroups when a finisher's reads would be long: a tile group spans three workgroups or more (so all
+// are split) and its partials hold (P / TG + 1) x T x G >= 48 vectors per thread. They start only as streaming
+// workgroups leave their CUs (a streaming workgroup's registers fill its CU) and see the count a memory round
+// trip later, about 2 us after the last arrival, which pays off only when one finisher's reads take longer
+// (measured: down 5120 x 17408 at M = 68 gains 13 %, the NVFP4 25600-wide fc at M = 16 2 %; the same down at
+// M = 17 or 1, or K = 6144 at M = 68, lose). The results are the same either way.
+bool finish_wgs(const StreamArgs& a) {
+  const int G = cdiv(a.M, 16);
+  return a.P >= 3 * a.TG && (a.P / a.TG + 1) * a.T * G >= 48;
+}
+
 // A fixed scratch region in place of the workspace (the no-allocation entry point): partials and counters, with
 // their capacities; the launch is rejected when it needs more.
 struct FixedScratch {
@@ -964,11 +991,13 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
     return LQ_OK;
   }
   if (rc) return rc;
+  a.NR = static_cast<short>(finish_wgs(a) ? kFinishShares : 0);
+  const size_t ncnt = static_cast<size_t>(a.TG) * (a.NR ? 2 : 1);
   const size_t pbytes = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float);
   if (fixed) {
-    if (pbytes > fixed->partial_bytes || static_cast<size_t>(a.TG) > fixed->counter_count)
+    if (pbytes > fixed->partial_bytes || ncnt > fixed->counter_count)
       return fail(LQ_ERR_SHAPE, std::string(name) + ": the launch needs " + std::to_string(pbytes) +
-                                    " bytes of partial sums and " + std::to_string(a.TG) +
+                                    " bytes of partial sums and " + std::to_string(ncnt) +
                                     " counters; the fixed scratch holds " + std::to_string(fixed->partial_bytes) +
                                     " and " + std::to_string(fixed->counter_count));
     a.partials = fixed->partials;
@@ -976,7 +1005,7 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   } else {
     Workspace* ws = workspace_for_current_device();
     if (!ws) return LQ_ERR_DEVICE;
-    rc = ws->reserve_stream(pbytes, static_cast<size_t>(a.TG));
+    rc = ws->reserve_stream(pbytes, ncnt);
     if (rc) return rc;
     a.partials = ws->partials;
     a.counters = ws->counters;
