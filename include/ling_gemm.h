@@ -157,8 +157,10 @@ int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const 
 int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate, const uint8_t* w_up,
                          const float* s_up, const uint8_t* w_down, const float* s_down, const uint16_t* resid,
                          uint16_t* h, uint16_t* y, int I, int H, void* stream);
-/* Synchronous: *hit = 1 if a stream_fp8_pc_ffn launch on the current device gave up its in-kernel wait at the
- * deadline since the last call (the results of such a launch are not valid), else 0; the call clears the flag.
+/* Synchronous: *hit = 1 if, since the last call, a launch on the current device gave up an in-kernel wait at its
+ * deadline: a stream_fp8_pc_ffn launch's wait for h (100 ms), or a skinny launch's finish workgroups' wait for the
+ * streaming workgroups (1 s, reached only if the GPU stops the launch that long); the results of such a launch
+ * are not valid. Else 0. The call clears the flags.
  * A caller of lq_stream_fp8_pc_ffn that cannot rule out a concurrent kernel holding CUs checks it after
  * synchronizing. No counterpart in the reference (its wait traps). */
 int lq_stream_ffn_deadline_status(int* hit);

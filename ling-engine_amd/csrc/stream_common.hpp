@@ -485,9 +485,12 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
 // have seen the full count (counters[TG + tg] counts them), the last one clears both counters for the next
 // launch. A finish workgroup never holds up a streaming one: the dispatcher places workgroups in index order, so
 // every streaming workgroup has its CU before any finish workgroup starts waiting. The wait gives up after a
-// second (s_memrealtime at 100 MHz), which a launch whose streaming workgroups run never reaches.
+// second (s_memrealtime at 100 MHz), which a launch whose streaming workgroups run never reaches; if it does
+// (the GPU preempted for that long), the workgroup records it in g_wait_expired (reported and cleared by
+// lq_stream_ffn_deadline_status) and finishes anyway, so the counters stay consistent for later launches.
 constexpr int kFinishShares = 4;
 constexpr unsigned long long kFinishWaitTicks = 100'000'000ull;
+__device__ int g_wait_expired = 0;  // per device: a bounded in-kernel wait gave up (results not valid)
 
 template <int G, int T, bool PAIR, bool OUTF32>
 __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
@@ -562,7 +565,10 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg, __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_AGENT)) < n) {
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kFinishWaitTicks) break;
+      if (__builtin_amdgcn_s_memrealtime() - t0 > kFinishWaitTicks) {
+        __hip_atomic_store(&g_wait_expired, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
       __builtin_amdgcn_s_sleep(16);
     }
   }

@@ -1327,14 +1327,20 @@ int lq_stream_ffn_deadline_status(int* hit) {
   Workspace* ws = workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
   *hit = 0;
-  if (!ws->sync) return LQ_OK;
-  if (hipMemcpy(hit, ws->sync + 2, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
-    return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: copy failed");
-  if (*hit) {  // reading clears it: a later report names only launches after this one
-    const int zero = 0;
-    if (hipMemcpy(ws->sync + 2, &zero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+  // reading clears the flags: a later report names only launches after this one
+  const int zero = 0;
+  if (ws->sync) {
+    if (hipMemcpy(hit, ws->sync + 2, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+      return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: copy failed");
+    if (*hit && hipMemcpy(ws->sync + 2, &zero, sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
       return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: clear failed");
   }
+  int fin = 0;  // a finish workgroup's wait
+  if (hipMemcpyFromSymbol(&fin, HIP_SYMBOL(g_wait_expired), sizeof(int)) != hipSuccess)
+    return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: copy failed");
+  if (fin && hipMemcpyToSymbol(HIP_SYMBOL(g_wait_expired), &zero, sizeof(int)) != hipSuccess)
+    return fail(LQ_ERR_DEVICE, "stream_ffn_deadline_status: clear failed");
+  *hit = *hit || fin;
   return LQ_OK;
 }
 
