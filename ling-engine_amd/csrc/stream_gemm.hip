@@ -381,9 +381,6 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   __syncthreads();
   const bool doit[2] = {last_flag[0] != 0, last_flag[1] != 0};
   LQ_TS(4);
-#ifdef LQ_STREAM_TRACE
-  ts[15] = (doit[0] ? 1 : 0) + (doit[1] ? 2 : 0) + 4 * (si[0].pl - si[0].pf + 1) + 256 * (si[1].pl - si[1].pf + 1);
-#endif
   if (!doit[0] && !doit[1]) {
     flush_trace(p);
     return;
