@@ -449,3 +449,26 @@ def test_multi_is_bit_identical_to_separate_launches(L, K):
         L.stream_gemm_multi(True, xh, xinv, [(w, tab, g, y, N) for (w, tab, g, N), y in zip(f4, ys)], K)
         for i, y in enumerate(ys):
             assert np.array_equal(y.view(torch.int32).cpu().numpy(), sep4[i]), f"nvfp4 multi M={M} matrix {i}"
+
+
+def test_multi_with_finish_workgroups_is_bit_identical(L):
+    """A multi launch whose split-K sums are done by finish workgroups (K = 17408 at M = 68: tile groups spread
+    over many workgroups, long reductions) equals separate launches bit for bit, and M = 68's first rows equal an
+    M = 17 launch, which finishes through its last arrivals."""
+    K = 17408
+    x = O.normal_f32(171, 1.0, (68, K))
+    ws = []
+    for i, N in enumerate((5120, 2048)):
+        q, _ = fp8_weights(180 + i, N, K)
+        ws.append((L.retile_fp8(to_dev(q)), 0.5 + i, N))
+    outs = {}
+    for M in (68, 17):
+        xh, xinv = L.to_half_rows(to_dev(x[:M]))
+        sep = [L.stream_gemm_fp8(xh, xinv, w, sc, N, K).view(torch.int32).cpu().numpy() for w, sc, N in ws]
+        ys = [torch.empty((M, N), dtype=torch.float32, device=DEV) for _, _, N in ws]
+        L.stream_gemm_multi(False, xh, xinv, [(w, None, sc, y, N) for (w, sc, N), y in zip(ws, ys)], K)
+        for i, y in enumerate(ys):
+            assert np.array_equal(y.view(torch.int32).cpu().numpy(), sep[i]), f"multi M={M} matrix {i}"
+        outs[M] = sep
+    for i in range(len(ws)):
+        assert np.array_equal(outs[68][i][:17], outs[17][i]), f"row invariance matrix {i}"
