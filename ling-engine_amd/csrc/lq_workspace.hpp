@@ -29,6 +29,15 @@ struct Workspace {
   int set_external(void* buf, size_t bytes);
 };
 
+// Bytes of split-K partial sums a skinny launch with up to `rows` activation rows can need on a device with `cus`
+// CUs: two slots per workgroup of at most 4 tiles x G groups x 4 floats x 256 threads, and up to 4 x cus
+// workgroups (a multi launch splits each of its up to 4 matrices over its own workgroups; the one-launch FFN's
+// two phases at 2 tiles each take less).
+inline size_t stream_partial_bound(size_t cus, int rows) {
+  const size_t G = static_cast<size_t>((rows + 15) / 16);
+  return 2 * 4 * cus * 4 * G * 4 * 256 * sizeof(float);
+}
+
 // The calling thread's current device's workspace (created on first call), or null (error set).
 Workspace* workspace_for_current_device();
 // Reserves the prefill's tail-split scratch at its bound (one FP32 tile per CU, one counter per CU), once.

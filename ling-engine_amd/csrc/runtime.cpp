@@ -157,11 +157,7 @@ size_t lq_stream_workspace_bytes(int max_rows) {
   if (max_rows < 1 || max_rows > LQ_MAX_STREAM_ROWS) return 0;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
-  const size_t P = static_cast<size_t>(lq::device_cus(dev));
-  const size_t G = static_cast<size_t>((max_rows + 15) / 16);
-  // two slots per workgroup of at most 4 tiles x G groups x 4 floats x 256 threads (the one-launch FFN's two
-  // phases at 2 tiles each take the same)
-  return lq::kExtHead + 2 * P * 4 * G * 4 * 256 * sizeof(float);
+  return lq::kExtHead + lq::stream_partial_bound(static_cast<size_t>(lq::device_cus(dev)), max_rows);
 }
 
 int lq_set_workspace(void* buffer, size_t bytes) {
@@ -173,7 +169,11 @@ int lq_set_workspace(void* buffer, size_t bytes) {
 int lq_init(void) {
   lq::Workspace* ws = lq::workspace_for_current_device();
   if (!ws) return LQ_ERR_DEVICE;
-  int rc = ws->external ? LQ_OK : ws->reserve_stream(size_t(64) << 20, size_t(1) << 16);
+  // the bound of any skinny launch, so that no later call allocates (graph capture)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return lq::fail(LQ_ERR_DEVICE, "lq_init: no current device");
+  const size_t bound = lq::stream_partial_bound(static_cast<size_t>(lq::device_cus(dev)), LQ_MAX_STREAM_ROWS);
+  int rc = ws->external ? LQ_OK : ws->reserve_stream(std::max(bound, size_t(64) << 20), size_t(1) << 16);
   if (rc) return rc;
   rc = lq::reserve_prefill_scratch(ws);
   if (rc) return rc;

@@ -472,3 +472,31 @@ def test_multi_with_finish_workgroups_is_bit_identical(L):
         outs[M] = sep
     for i in range(len(ws)):
         assert np.array_equal(outs[68][i][:17], outs[17][i]), f"row invariance matrix {i}"
+
+
+def test_caller_workspace_holds_a_full_multi_launch(L):
+    """lq_stream_workspace_bytes covers the largest skinny launch: a multi launch of four NVFP4 matrices (four tiles
+    per wave) at M = 68, each matrix on its own workgroups, so up to four times #CUs workgroups' partials. The
+    results equal those from the library's own workspace."""
+    K, M = 5120, 68
+    x = O.normal_f32(191, 1.0, (M, K))
+    xh, xinv = L.to_half_rows(to_dev(x))
+    mats = []
+    for i in range(4):
+        v, sc, g, _ = O.quant_nvfp4(O.normal_bf16(192 + i, 0.02, (2048, K)))
+        mats.append((L.retile_nvfp4(to_dev(v), to_dev(sc)), g))
+
+    def run():
+        ys = [torch.empty((M, 2048), dtype=torch.float32, device=DEV) for _ in mats]
+        L.stream_gemm_multi(True, xh, xinv, [(w, None, g, y, 2048) for (w, g), y in zip(mats, ys)], K)
+        torch.cuda.synchronize()
+        return [y.view(torch.int32).cpu() for y in ys]
+
+    own = run()
+    buf = torch.empty(L.stream_workspace_bytes(M), dtype=torch.uint8, device=DEV)
+    try:
+        L.set_workspace(buf)
+        got = run()
+    finally:
+        L.set_workspace(None)
+    assert all(torch.equal(a, b) for a, b in zip(own, got))
