@@ -345,6 +345,19 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     if (splitF) publish_partial<G, T>(a, p, 0, accF, r);
     else epilogue<G, PAIR, OUTF32, T, YCOH>(a, sF.mi, sF.wtile0, accF, eF, r, t);
   }
+  // Where tile groups span two workgroups or more, a workgroup with two partials counts its first group's
+  // arrival before it publishes the second: otherwise it arrives last at both groups more often than not (it has
+  // the most to publish) and then finishes both in a row, the slowest finish there is (measured: down at M=17 and
+  // the M=68 projections 3-6 % faster). The gate|up pair, where nearly every workgroup has two partials, keeps
+  // the single wait (the extra one measured 1 % slower there).
+  const bool early = !PAIR && !a.NR && splitF && splitL && seg.P >= 2 * (seg.U / a.C);
+  int oldF = 0;
+  if (early) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      oldF = __hip_atomic_fetch_add(a.counters + tg_first, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (splitL) publish_partial<G, T>(a, p, one ? 0 : 1, accL, r);
   else epilogue<G, PAIR, OUTF32, T, YCOH>(a, sL.mi, sL.wtile0, accL, eL, r, t);
   if (!splitF && !splitL) {
@@ -372,7 +385,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     const int span = h ? si[1].pl - si[1].pf : si[0].pl - si[0].pf;
     int last = 0;
     if (h ? splitL : splitF) {
-      const int old = __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int old = (!h && early) ? oldF
+                                    : __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = old == span;
       if (last) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
