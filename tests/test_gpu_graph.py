@@ -143,3 +143,36 @@ def test_prefill_scratch_is_not_reallocated(L):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {rep} after the larger shape"
+
+
+def test_finish_workgroups_under_graph_replay(L):
+    """A launch whose split-K sums are done by finish workgroups (M = 68, a long K over few tile groups): its
+    arrival and finish counters reset themselves, so every replay equals an eager launch on the same inputs."""
+    M, N, K = 68, 1024, 8192
+    q, s = O.quant_fp8_per_channel(O.normal_f32(121, 0.02, (N, K)))
+    tw, sd = L.retile_fp8(to_dev(q)), to_dev(s)
+    x = torch.empty((M, K), dtype=torch.bfloat16, device=DEV)
+    r = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    x.copy_(bf16(122, (M, K)))
+    r.copy_(bf16(123, (M, N)))
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        L.stream_fp8_pc_residual(x, tw, sd, r, N, y=y)  # warm-up on the capture stream
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        L.stream_fp8_pc_residual(x, tw, sd, r, N, y=y)
+    for rep in range(4):
+        x.copy_(bf16(130 + rep, (M, K)))
+        r.copy_(bf16(140 + rep, (M, N)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = y.view(torch.int16).clone()
+        ye = L.stream_fp8_pc_residual(x, tw, sd, r, N)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ye.view(torch.int16)), f"replay {rep}"
+    assert L.stream_ffn_deadline_status() == 0
