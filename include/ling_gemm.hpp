@@ -140,6 +140,11 @@ inline void rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, 
                           float input_scale, uint8_t* q, uint8_t* sf, hipStream_t s) {
   lq_check(lq_rmsnorm_quant(x, w, out, M, H, eps, nvfp4 ? 1 : 0, input_scale, q, sf, s));
 }
+// kernels.cuh:234-235 (BF16 as uint16_t bits)
+inline void rmsnorm_quant_bf16(const float* x, const uint16_t* w, uint16_t* out, int M, int H, float eps, bool nvfp4,
+                               float input_scale, uint8_t* q, uint8_t* sf, hipStream_t s) {
+  lq_check(lq_rmsnorm_quant_bf16(x, w, out, M, H, eps, nvfp4 ? 1 : 0, input_scale, q, sf, s));
+}
 
 // ---- prefill (block-scaled FP8; kernels.cuh:190-221 for the reference's per-tensor forms) ----
 inline void quant_act_fp8_g128(const uint16_t* x_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t s) {
@@ -147,6 +152,10 @@ inline void quant_act_fp8_g128(const uint16_t* x_bf16, int M, int K, uint8_t* q,
 }
 inline void quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q, hipStream_t s) {
   lq_check(lq_quant_act_fp8(x, M, K, input_scale, q, s));
+}
+// kernels.cuh:237
+inline void quant_act_fp8_bf16in(const uint16_t* x_bf16, int M, int K, float input_scale, uint8_t* q, hipStream_t s) {
+  lq_check(lq_quant_act_fp8_bf16in(x_bf16, M, K, input_scale, q, s));
 }
 inline void prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
                              bool accumulate, hipStream_t s) {
@@ -159,6 +168,21 @@ inline void prefill_gemm_fp8_bf16out(const uint8_t* xq, int M, const uint8_t* w,
 inline void prefill_gemm_fp8_block(const uint8_t* xq, const float* xs, int M, const uint8_t* w, const float* ws,
                                    uint16_t* y_bf16, int ldy, int N, int K, hipStream_t s) {
   lq_check(lq_prefill_fp8_block(xq, xs, M, w, ws, y_bf16, ldy, N, K, s));
+}
+
+// ---- host weight quantizers (CPU threads; model.cu:188-249 quantize_nvfp4, and the configs' FP8 recipes) ----
+// Returns g (scale2); rel_sq_err may be null.
+inline float quantize_nvfp4(const uint16_t* w_bf16, int N, int K, uint8_t* values, uint8_t* scales,
+                            double* rel_sq_err = nullptr) {
+  float g = 0.f;
+  lq_check(lq_quantize_nvfp4(w_bf16, N, K, values, scales, &g, rel_sq_err));
+  return g;
+}
+inline void quantize_fp8_channel(const void* w, int dtype, int N, int K, uint8_t* q, float* scale) {
+  lq_check(lq_quantize_fp8_channel(w, dtype, N, K, q, scale));
+}
+inline void quantize_fp8_block128(const void* w, int dtype, int N, int K, uint8_t* q, float* scale) {
+  lq_check(lq_quantize_fp8_block128(w, dtype, N, K, q, scale));
 }
 
 }  // namespace ling::kernels

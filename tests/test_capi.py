@@ -94,6 +94,23 @@ int main() {
       if (std::strcmp(e.what(), want[c]) != 0) { std::printf("got '%s'\n", e.what()); ++fails; }
     }
   }
+  // host quantizers (CPU only): an all-zero matrix has g = 1 and zero codes; 448 and -224 on one channel of
+  // scale 1 encode as 0x7e and 0xf6 (E4M3 1.75 x 2^8, -1.75 x 2^7)
+  uint16_t wz[16 * 16] = {};
+  uint8_t v[16 * 8], sc[16];
+  if (K::quantize_nvfp4(wz, 16, 16, v, sc) != 1.f) ++fails;
+  for (int i = 0; i < 16 * 8; ++i) if (v[i]) ++fails;
+  float w1[2] = {448.f, -224.f};
+  uint8_t q1[2];
+  float s1 = 0.f;
+  K::quantize_fp8_channel(w1, LQ_DT_F32, 1, 2, q1, &s1);
+  if (s1 != 1.f || q1[0] != 0x7e || q1[1] != 0xf6) ++fails;
+  try {
+    K::quantize_nvfp4(wz, 16, 8, v, sc);
+    ++fails;
+  } catch (const std::runtime_error& e) {
+    if (std::strcmp(e.what(), "quantize_nvfp4: K must be a positive multiple of 16") != 0) ++fails;
+  }
   std::printf("fails=%d\n", fails);
   return fails;
 }
