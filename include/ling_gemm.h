@@ -205,8 +205,9 @@ int lq_rmsnorm_quant_bf16(const float* x, const uint16_t* w, uint16_t* out, int 
 
 /* ---------------- prefill, block-scaled FP8 (additive; reference src/core/kernels.cuh:190-221) ---------------- */
 /* BF16 x [M][K] -> FP8 E4M3 q [M][K] with one FP32 scale per 1x128 group, scale [M][K/128] = amax / 448 (1 for an
- * all-zero group), q = E4M3_rne(x / scale); x 16-byte and q 8-byte aligned. The block-scaled counterpart of
- * quant_act_fp8 (kernels.cuh:199). */
+ * all-zero group), q = E4M3_rne_sat(x * (1 / scale)) (reciprocal and product rounded to FP32, as quant_act_fp8
+ * multiplies by 1 / input_scale); x 16-byte and q 8-byte aligned. The block-scaled counterpart of quant_act_fp8
+ * (kernels.cuh:199). */
 int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* scale, void* stream);
 /* y[M][0..N) (rows ldy apart, BF16) = bf16(sum over 128-value K blocks kb of (xq . W^T over kb) * xs[m][kb] *
  * ws[n/128][kb]); xq FP8 [M][K], xs FP32 [M][K/128], W tiled FP8 (the stream GEMMs' blob), ws FP32 [N/128][K/128].

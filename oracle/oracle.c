@@ -250,7 +250,11 @@ void or_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* s
       for (int c = 0; c < 128; ++c) amax = fmaxf(amax, fabsf(or_bf16_float(x[base + c])));
       const float s = amax > 0.f ? amax / 448.f : 1.f;
       scale[(size_t)m * KB + kb] = s;
-      for (int c = 0; c < 128; ++c) q[base + c] = or_e4m3_encode(or_bf16_float(x[base + c]) / s);
+      const float r = 1.f / s;  /* x times the reciprocal, each rounded to FP32 (the library's definition) */
+      for (int c = 0; c < 128; ++c) {
+        const float v = or_bf16_float(x[base + c]) * r;
+        q[base + c] = or_e4m3_encode(v);
+      }
     }
 }
 

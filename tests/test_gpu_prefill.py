@@ -404,10 +404,10 @@ def test_rmsnorm_quant_row_widths(L):
 
 
 def test_quant_act_fp8_g128_rounding_boundaries(L):
-    """Quotients x / s on and next to E4M3 rounding midpoints (the quantizer's reciprocal shortcut must fall back to
-    the division there): groups with s = 3 exactly (amax 1344) holding 3 x every midpoint of [2^-9, 448], groups
-    with an inexact s (amax 1000) holding the BF16 values nearest to midpoint x s and their BF16 neighbours, and
-    groups of tiny and huge magnitudes."""
+    """Scaled values x * (1 / s) on and next to E4M3 rounding midpoints, where one FP32 rounding decides the code:
+    groups with s = 3 exactly (amax 1344) holding 3 x every midpoint of [2^-9, 448], groups with an inexact s
+    (amax 1000) holding the BF16 values nearest to midpoint x s and their BF16 neighbours, and groups of tiny and
+    huge magnitudes."""
     codes = np.arange(0, 0x7f, dtype=np.uint8)
     vals = np.array([_e4m3(c) for c in codes], np.float32)
     mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2)

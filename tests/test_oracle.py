@@ -149,6 +149,13 @@ def test_fp8_block_quantizers_reconstruct():
     zero = np.zeros((1, 128), np.uint16)
     zq, zs = O.quant_act_fp8_g128(zero)
     assert zs[0, 0] == 1.0 and np.all(zq == 0)
+    # the codes: torch's E4M3 cast (round to nearest even) of x * (1 / s), each rounded to FP32, clamped to 448
+    for m in range(4):
+        for kb in range(2):
+            r = np.float32(1) / xs[m, kb]
+            v = np.clip(xf[m, kb * 128:(kb + 1) * 128] * r, np.float32(-448), np.float32(448)).astype(np.float32)
+            want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            assert np.array_equal(xq[m, kb * 128:(kb + 1) * 128], want)
 
 
 def test_tiled_fp8_literal_positions():
