@@ -15,15 +15,6 @@
 namespace lq {
 namespace {
 
-// E2M1 nearest, ties to the even code (values 0, .5, 1, 1.5, 2, 3, 4, 6): each term counts a midpoint passed,
-// strictly above it when the lower code is the even one, from it when the upper one is.
-__device__ __forceinline__ uint32_t e2m1_rne(float y) {
-  const float a = fabsf(y);
-  uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.f);
-  if (isnan(a)) c = 7;
-  return c | (signbit(y) ? 8u : 0u);
-}
-
 // E4M3, round to nearest even, saturating to +-448 (NaN stays NaN).
 __device__ __forceinline__ uint32_t e4m3_sat(float v) {
   return __builtin_amdgcn_cvt_pk_fp8_f32(isnan(v) ? v : fminf(fmaxf(v, -448.f), 448.f), 0.f, 0, false) & 0xffu;
@@ -44,7 +35,7 @@ __device__ __forceinline__ void put_nvfp4_block(const float (&v)[16], float g, u
   uint32_t w[2] = {0u, 0u};
 #pragma unroll
   for (int i = 0; i < 16; i += 2) {
-    const uint32_t byte = e2m1_rne(v[i] * os) | (e2m1_rne(v[i + 1] * os) << 4);
+    const uint32_t byte = e2m1x2_rne(v[i] * os, v[i + 1] * os);
     w[i >> 3] |= byte << (8 * ((i >> 1) & 3));
   }
   *reinterpret_cast<u32x2*>(q8) = u32x2{w[0], w[1]};

@@ -80,13 +80,6 @@ __device__ __forceinline__ u32x4 deq_word(uint32_t d, uint32_t sc, int s) {
                __builtin_bit_cast(uint32_t, e3)};
 }
 
-__device__ __forceinline__ uint32_t e2m1_rne(float y) {
-  const float a = fabsf(y);
-  uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.f);
-  if (isnan(a)) c = 7;
-  return c | (signbit(y) ? 8u : 0u);
-}
-
 #define LQ_WAIT_VM(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
 
 template <bool SWIGLU>
@@ -267,8 +260,8 @@ __global__ void __launch_bounds__(kThreads) prefill_nvfp4_kernel(const Nvfp4Args
             const int m = m0 + wm * 64 + 16 * j + r;
             if (m < a.M && ncol < a.N) {
               uint8_t* qr = a.q_out + static_cast<size_t>(m) * (a.N / 2) + ncol / 2 + 2 * t;
-              const uint32_t b0 = e2m1_rne(v[0] * os) | (e2m1_rne(v[1] * os) << 4);
-              const uint32_t b1 = e2m1_rne(v[2] * os) | (e2m1_rne(v[3] * os) << 4);
+              const uint32_t b0 = e2m1x2_rne(v[0] * os, v[1] * os);
+              const uint32_t b1 = e2m1x2_rne(v[2] * os, v[3] * os);
               *reinterpret_cast<uint16_t*>(qr) = static_cast<uint16_t>(b0 | (b1 << 8));
               if (t == 0) a.sf_out[static_cast<size_t>(m) * (a.N / 16) + ncol / 16] = static_cast<uint8_t>(sc);
             }

@@ -435,3 +435,28 @@ def test_quant_act_fp8_g128_rounding_boundaries(L):
 def _e4m3(c):
     e, m = (int(c) >> 3) & 15, int(c) & 7
     return (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+
+
+def test_quant_act_nvfp4_rounding_boundaries(L):
+    """E2M1 codes at their rounding boundaries: with input scale 1 and a block whose largest magnitude is 6, the
+    block scale is E4M3(1) and every value is encoded unscaled, so blocks holding each E2M1 midpoint (0.25, 0.75,
+    1.25, 1.75, 2.5, 3.5, 5), its BF16 neighbours, both signs, zeros, -0 and small negatives test the
+    round-to-nearest-even encoding (ties to the even code) bit for bit against the oracle."""
+    mids = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+    b = O.f32_to_bf16(mids)
+    vals = np.concatenate([b, b + 1, b - 1]).astype(np.uint16)
+    vals = O.bf16_to_f32(vals)
+    pool = np.concatenate([vals, -vals, np.array([0.0, -0.0, -0.1, -1e-8, 1e-8, 6.0, -6.0, 0.5, 3.0], np.float32)])
+    blocks = []
+    for i in range(0, len(pool), 15):
+        blk = np.zeros(16, np.float32)
+        part = pool[i:i + 15]
+        blk[:len(part)] = part
+        blk[15] = 6.0  # the block's largest magnitude: scale E4M3(6 / 6) = 1
+        blocks.append(blk)
+    x = np.concatenate(blocks)
+    x = np.resize(x, -(-x.size // 256) * 256).reshape(-1, 256).astype(np.float32)
+    q, sf = L.quant_act_nvfp4(to_dev(x), 1.0)
+    rq, rsf = O.quant_act_nvfp4(x, 1.0)
+    assert np.array_equal(sf.cpu().numpy(), rsf), "scales"
+    assert np.array_equal(q.cpu().numpy(), rq), "codes"
