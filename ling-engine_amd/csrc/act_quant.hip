@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(256) quant_nvfp4_kernel(const float* __restric
 // so H <= 65536), the row held in registers from a single read: the sum of squares (each thread's values in
 // order, then the wave, then the waves in order), rstd = 1 / sqrt(sum / H + eps), v = x * rstd * (1 + w)
 // (written to `out` when given), then the thread quantizes its blocks of BF16(v): NVFP4, or FP8
-// E4M3(BF16(v) / input_scale).
+// E4M3(BF16(v) * (1 / input_scale)).
 // BF16OUT: `out` is BF16, the values rounded as the quantizer rounds them (reference rmsnorm_quant_bf16,
 // prefill_gemm.cu:640-645, the norm_quant_kernel's OutT = BF16 form).
 template <bool FP4, int NB, bool BF16OUT>

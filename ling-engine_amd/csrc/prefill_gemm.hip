@@ -330,39 +330,42 @@ __global__ void __launch_bounds__(kThreads) prefill_fp8_kernel(const PrefillArgs
 // to that rounding; clamped, which is the saturating conversion.
 __global__ void __launch_bounds__(256) quant_fp8_g128_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                              uint8_t* __restrict__ q, float* __restrict__ scale) {
+  // blockIdx.x: 16 groups of a row; blockIdx.y + k gridDim.y: the rows (no integer division per thread)
   const int KB = K / 128;
-  const long long grp = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+  const int kb = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
-  const bool ok = grp < static_cast<long long>(M) * KB;  // the 16 lanes of a group agree
-  const int m = ok ? static_cast<int>(grp / KB) : 0, kb = ok ? static_cast<int>(grp % KB) : 0;
-  const size_t base = static_cast<size_t>(m) * K + static_cast<size_t>(kb) * 128 + 8 * sub;
-  u32x4 raw = u32x4{0u, 0u, 0u, 0u};
-  if (ok) raw = *reinterpret_cast<const u32x4*>(x + base);
-  float v[8];
+  const bool ok = kb < KB;  // the 16 lanes of a group agree
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const size_t base = static_cast<size_t>(m) * K + static_cast<size_t>(kb) * 128 + 8 * sub;
+    u32x4 raw = u32x4{0u, 0u, 0u, 0u};
+    if (ok) raw = *reinterpret_cast<const u32x4*>(x + base);
+    float v[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = bf16_to_f32(raw[i] & 0xffff);
-    v[2 * i + 1] = bf16_to_f32(raw[i] >> 16);
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_to_f32(raw[i] & 0xffff);
+      v[2 * i + 1] = bf16_to_f32(raw[i] >> 16);
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const float s = mx > 0.f ? mx / 448.f : 1.f;
+    const float rs = 1.f / s;
+    uint32_t w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float a[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[i] = fminf(fmaxf(v[4 * h + i] * rs, -448.f), 448.f);
+      const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0, false);
+      w[h] = __builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], lo, true);
+    }
+    if (ok) {
+      *reinterpret_cast<u32x2*>(q + base) = u32x2{w[0], w[1]};
+      if (sub == 0) scale[static_cast<size_t>(m) * KB + kb] = s;
+    }
   }
-  float mx = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
-#pragma unroll
-  for (int o = 8; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  const float s = mx > 0.f ? mx / 448.f : 1.f;
-  const float rs = 1.f / s;
-  uint32_t w[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    float a[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = fminf(fmaxf(v[4 * h + i] * rs, -448.f), 448.f);
-    const uint32_t lo = __builtin_amdgcn_cvt_pk_fp8_f32(a[0], a[1], 0, false);
-    w[h] = __builtin_amdgcn_cvt_pk_fp8_f32(a[2], a[3], lo, true);
-  }
-  if (!ok) return;
-  *reinterpret_cast<u32x2*>(q + base) = u32x2{w[0], w[1]};
-  if (sub == 0) scale[static_cast<size_t>(m) * KB + kb] = s;
 }
 
 // Per-tensor FP8 activation quantizer (reference src/core/prefill_gemm.cu:496-511): each value rounded to BF16
@@ -469,8 +472,8 @@ int lq_quant_act_fp8_g128(const uint16_t* x, int M, int K, uint8_t* q, float* sc
   if (!x || !q || !scale) return fail(LQ_ERR_ARG, "quant_act_fp8_g128: null pointer");
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q) % 8 != 0)
     return fail(LQ_ERR_ARG, "quant_act_fp8_g128: x must be 16-byte and q 8-byte aligned");
-  const long long groups = static_cast<long long>(M) * (K / 128);
-  hipLaunchKernelGGL(quant_fp8_g128_kernel, dim3(static_cast<unsigned>((groups + 15) / 16)), dim3(256), 0,
+  const unsigned rows = static_cast<unsigned>(std::min(M, 65535));
+  hipLaunchKernelGGL(quant_fp8_g128_kernel, dim3(static_cast<unsigned>((K / 128 + 15) / 16), rows), dim3(256), 0,
                      static_cast<hipStream_t>(stream), x, M, K, q, scale);
   return check_launch("quant_act_fp8_g128");
 }
