@@ -43,7 +43,8 @@ struct StreamArgs {
   int TG;             // tile groups (all segments)
   short T;            // tiles per wave (the kernel's template argument)
   short NR;           // finish workgroups per split tile group (0: the last workgroup to arrive finishes it)
-  int count;          // matrices
+  short count;        // matrices
+  short wait_ms;      // finish workgroups: how long to wait for the arrivals before giving up (milliseconds)
   const uint8_t* w[kMaxMats];
   const uint8_t* table[kMaxMats];   // coded NVFP4: device scale-code table [64]
   const float* svec[kMaxMats];      // per-channel scales [N] or null
@@ -485,11 +486,12 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
 // have seen the full count (counters[TG + tg] counts them), the last one clears both counters for the next
 // launch. A finish workgroup never holds up a streaming one: the dispatcher places workgroups in index order, so
 // every streaming workgroup has its CU before any finish workgroup starts waiting. The wait gives up after a
-// second (s_memrealtime at 100 MHz), which a launch whose streaming workgroups run never reaches; if it does
+// second (StreamArgs::wait_ms, on s_memrealtime at 100 MHz), which a launch whose streaming workgroups run never
+// reaches; if it does
 // (the GPU preempted for that long), the workgroup records it in g_wait_expired (reported and cleared by
-// lq_stream_ffn_deadline_status) and finishes anyway, so the counters stay consistent for later launches.
+// lq_stream_ffn_deadline_status) and finishes anyway; the arrival counter is then brought back by subtracting the
+// expected count, so late arrivals leave it at zero for later launches.
 constexpr int kFinishShares = 4;
-constexpr unsigned long long kFinishWaitTicks = 100'000'000ull;
 __device__ int g_wait_expired = 0;  // per device: a bounded in-kernel wait gave up (results not valid)
 
 template <int G, int T, bool PAIR, bool OUTF32>
@@ -565,7 +567,7 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg, __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_AGENT)) < n) {
-      if (__builtin_amdgcn_s_memrealtime() - t0 > kFinishWaitTicks) {
+      if (__builtin_amdgcn_s_memrealtime() - t0 > static_cast<unsigned long long>(a.wait_ms) * 100'000ull) {
         __hip_atomic_store(&g_wait_expired, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
@@ -577,7 +579,9 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
   if (threadIdx.x == 0) {
     const int old = __hip_atomic_fetch_add(a.counters + a.TG + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == kFinishShares - 1) {
-      __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // minus the n arrivals rather than a store of zero: after an expired wait, arrivals still to come bring the
+      // counter back to exactly zero instead of leaving a count for the next launch
+      __hip_atomic_fetch_add(a.counters + tg, -n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(a.counters + a.TG + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }

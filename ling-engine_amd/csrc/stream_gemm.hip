@@ -34,6 +34,7 @@
 #include "stream_common.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <cstdlib>
 #include <cstring>
@@ -870,6 +871,7 @@ int launch_m(const StreamArgs& a, hipStream_t s) {
 
 // Validates, fills the launch arguments and launches. `fmt`: weight format; `f16`: activations are an
 // FP16 row copy (with xinv) rather than BF16; `pair`: mats = {gate, up} with the SiLU*mul epilogue.
+std::atomic<int> g_finish_wait_ms{1000};  // StreamArgs::wait_ms of later launches (lq_debug_finish_wait_ms)
 #ifdef LQ_STREAM_TRACE
 unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the next launches
 #endif
@@ -937,7 +939,7 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
   a.M = M;
   a.K = K;
   a.C = K / kChunk;
-  a.count = n;
+  a.count = static_cast<short>(n);
   int Ns[kMaxMats];
   for (int i = 0; i < n; ++i) {
     const Mat& m = mats[i];
@@ -1003,6 +1005,7 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   }
   if (rc) return rc;
   a.NR = static_cast<short>(finish_wgs(a) ? kFinishShares : 0);
+  a.wait_ms = static_cast<short>(g_finish_wait_ms.load(std::memory_order_relaxed));
   const size_t ncnt = static_cast<size_t>(a.TG) * (a.NR ? 2 : 1);
   const size_t pbytes = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float);
   if (fixed) {
@@ -1177,6 +1180,14 @@ int noalloc_init_current_device() {
 using namespace lq;
 
 extern "C" {
+
+// Test hook (not part of the interface): the finish workgroups' wait limit for later launches, in milliseconds
+// (default 1000; 0 makes a wait give up at its first unanswered poll, so tests can reach the expired-wait path
+// without a stalled GPU). Returns the previous limit, or -1 for a value outside [0, 32767].
+int lq_debug_finish_wait_ms(int ms) {
+  if (ms < 0 || ms > 32767) return -1;
+  return g_finish_wait_ms.exchange(ms);
+}
 
 #ifdef LQ_STREAM_TRACE
 // Trace builds only: stream launches record per-workgroup phase stamps into `buf` ([P][8] u64, device).

@@ -474,6 +474,36 @@ def test_multi_with_finish_workgroups_is_bit_identical(L):
         assert np.array_equal(outs[68][i][:17], outs[17][i]), f"row invariance matrix {i}"
 
 
+def test_expired_finish_wait_leaves_counters_consistent(L):
+    """Finish workgroups whose wait for the arrivals gives up (forced from the host with a zero wait limit through
+    the test hook lq_debug_finish_wait_ms; every kernel still runs to its end) leave the arrival counters
+    consistent: the status call reports an expiry once and clears it, and later launches with the normal limit
+    equal a launch made before, bit for bit."""
+    import ctypes
+    K, N, M = 17408, 5120, 68  # tile groups over ~6 workgroups at 5 activation groups: finish workgroups
+    x = O.normal_f32(201, 1.0, (M, K))
+    q, _ = fp8_weights(202, N, K)
+    w = L.retile_fp8(to_dev(q))
+    xh, xinv = L.to_half_rows(to_dev(x))
+    ref = L.stream_gemm_fp8(xh, xinv, w, 0.5, N, K).view(torch.int32).cpu().numpy()
+    assert L.stream_ffn_deadline_status() == 0
+    hook = L.lib.lq_debug_finish_wait_ms
+    hook.argtypes, hook.restype = [ctypes.c_int], ctypes.c_int
+    assert hook(-1) == -1
+    prev = hook(0)
+    try:
+        for _ in range(3):
+            L.stream_gemm_fp8(xh, xinv, w, 0.5, N, K)  # outputs not checked: a wait may give up
+        torch.cuda.synchronize()
+    finally:
+        assert hook(prev) == 0
+    print(f"expired finish waits reported: {L.stream_ffn_deadline_status()}", flush=True)
+    assert L.stream_ffn_deadline_status() == 0  # reading cleared the flag
+    for _ in range(3):
+        got = L.stream_gemm_fp8(xh, xinv, w, 0.5, N, K).view(torch.int32).cpu().numpy()
+        assert np.array_equal(got, ref)
+
+
 def test_caller_workspace_holds_a_full_multi_launch(L):
     """lq_stream_workspace_bytes covers the largest skinny launch: a multi launch of four NVFP4 matrices (four tiles
     per wave) at M = 68, each matrix on its own workgroups, so up to four times #CUs workgroups' partials. The
