@@ -152,6 +152,23 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     __builtin_amdgcn_sched_barrier(0);
     advance();
   };
+  // The same stage in two parts, as the main loops issue it: the activation share before the chunk's barrier,
+  // the weights after it. The activations of every wave then reach the memory pipeline while the waves gather at
+  // the barrier, instead of all of a chunk's loads leaving in one burst behind it (measured: the M=68 launches
+  // 3-5 % faster, M=17 about 1 %).
+  unsigned stage_oob = 0u;
+  auto load_stage_x = [&](int j) {
+    stage_oob = lleft > 0 ? 0u : 0x80000000u;
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(j, lc, stage_oob);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto load_stage_w = [&](int j) {
+    __builtin_amdgcn_sched_barrier(0);
+    load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | stage_oob), slot, stage_oob);
+    __builtin_amdgcn_sched_barrier(0);
+    advance();
+  };
   auto put_x = [&](int j, int sl) {
 #pragma unroll
     for (int i = 0; i < G; ++i) {
@@ -275,8 +292,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
         const int it = base + j;
         const int sl = (it + 1) % NSLOT;
         put_x((j + 1) % PF, sl);
+        load_stage_x((j + PF - 1) % PF);
         __syncthreads();
-        load_stage((j + PF - 1) % PF);
+        load_stage_w((j + PF - 1) % PF);
 #pragma unroll
         for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
         if constexpr (CVT) chunk_scales(scn, sl);
@@ -311,8 +329,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
       for (int j = 0; j < PF; ++j) {
         const int it = base + j;
         put_x(j, it & 1);
+        load_stage_x((j + PF - 1) % PF);
         __syncthreads();
-        load_stage((j + PF - 1) % PF);
+        load_stage_w((j + PF - 1) % PF);
         if (it < n_it) {
           const uint8_t* tab[T];
           tables(tab);
