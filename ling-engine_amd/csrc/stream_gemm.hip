@@ -929,6 +929,11 @@ int choose_tiles(const char* name, int fmt, bool pair, const int* Ns, int n, Str
     T0 = T;
     if (static_cast<long long>(tg) * a.C * (P + 1) >= (1LL << 31) || tgs + static_cast<long long>(tg) >= (1LL << 30))
       return fail(LQ_ERR_SHAPE, std::string(name) + ": matrices too large for one launch");
+    // the kernels address a weight blob and the activations with 32-bit byte offsets
+    const long long blk = fmt == kFp8 ? kTileBytesFp8 : fmt == kFp4 ? kTileBytesFp4 : kValueBytesFp4 + kCodeBytesFp4;
+    if (static_cast<long long>(Ns[i] / 16) * a.C * blk >= (1LL << 31) ||
+        static_cast<long long>(a.M) * a.C * kChunk * 2 >= (1LL << 31))
+      return fail(LQ_ERR_SHAPE, std::string(name) + ": weight blob and activations must be below 2^31 bytes");
     a.tg0[i] = tgs;
     a.wg0[i] = wgs;
     tgs += tg;
@@ -1330,6 +1335,8 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
     return fail(LQ_ERR_SHAPE, nm + ": K % 128 and cap % 32 must be 0");
   if (M < 1 || M > LQ_MAX_STREAM_ROWS) return fail(LQ_ERR_SHAPE, nm + ": M must be in [1, 80]");
   if (N <= 0 || N % 16 != 0) return fail(LQ_ERR_SHAPE, nm + ": N % 16 and K % 128 must be 0");
+  if (static_cast<long long>(N / 16) * (K / kChunk) * kTileBytesFp4 >= (1LL << 31))
+    return fail(LQ_ERR_SHAPE, nm + ": weight blob must be below 2^31 bytes");
   if (!xh || !xinv || !w || !rows || !nrows || !y) return fail(LQ_ERR_ARG, nm + ": null pointer");
   GatherArgs a{};
   a.x = xh;

@@ -365,6 +365,17 @@ def test_error_paths(L):
         L.stream_fp8_pc(bf16_dev(O.normal_bf16(1, 1.0, (2, 100))), tw, to_dev(s), 16)
     with pytest.raises(L.LingGemmError, match="N % 16"):
         L.stream_fp8_pc(x[:2].contiguous(), tw, to_dev(s), 24)
+    # a weight blob of 2 GiB or more is refused before launch (the kernels' byte offsets are 32-bit); the small
+    # buffers passed are never read
+    y = torch.empty((1, 16), dtype=torch.bfloat16, device=DEV)
+    rc = L.lib.lq_stream_fp8_pc(x.data_ptr(), 1, tw.data_ptr(), to_dev(s).data_ptr(), y.data_ptr(), 131072, 16384,
+                                None)
+    assert rc != 0 and b"2^31" in L.lib.lq_last_error()
+    rows = torch.zeros(32, dtype=torch.int32, device=DEV)
+    yg = torch.empty((1, 32), dtype=torch.float32, device=DEV)
+    rc = L.lib.lq_stream_gemm_gather_nvfp4(x.data_ptr(), yg.data_ptr(), 1, tw.data_ptr(), None, 1.0, rows.data_ptr(),
+                                           rows.data_ptr(), 32, yg.data_ptr(), 16384, 262144, None)
+    assert rc != 0 and b"2^31" in L.lib.lq_last_error()
 
 
 def test_caller_workspace(L):
