@@ -64,6 +64,13 @@ def test_errors_are_reported_before_any_launch():
     assert b"1 to 4 matrices per launch" in lib.lq_last_error()
     assert lib.lq_retile_fp8(None, None, 17, 128, None) == 1
     assert b"N % 16 and K % 128 must be 0" in lib.lq_last_error()
+    # prefill with no rows returns silently, as the reference's does (prefill_gemm.cu:596): no launch, no error
+    assert lib.lq_prefill_fp8_block(None, None, 0, None, None, None, 128, 128, 128, None) == 0
+    assert lib.lq_prefill_gemm_fp8(None, 0, None, 1.0, None, 128, 128, 128, 0, None) == 0
+    assert lib.lq_prefill_gemm_fp8_bf16out(None, 0, None, 1.0, None, 128, 128, 128, None) == 0
+    assert lib.lq_prefill_gemm_nvfp4(None, None, 0, None, 1.0, None, 128, 128, 128, 0, None, None) == 0
+    # but the shape rules still hold for it
+    assert lib.lq_prefill_fp8_block(None, None, 0, None, None, None, 64, 64, 128, None) == 1
 
 
 CPP = r"""
