@@ -539,7 +539,12 @@ struct GatherDepth {
   static constexpr int D = G == 1 ? 8 : G == 2 ? 4 : 2;  // chunks in flight: 16 * G * D activation VGPRs
 };
 
-template <int G>
+// ONE (M % 16 == 1: the last token group holds a single row, M - 1): that row's four 16-byte pieces of a chunk
+// come in one load (lane r < 4 takes piece r) and a row shift of the lanes hands piece s to lane 0; the other
+// lanes of the group get values of rows past M, whose MFMA columns are never stored. The MFMA operands of every
+// stored column are the same as with four loads, so the results are too; it saves three of the wave's loads per
+// chunk.
+template <int G, bool ONE>
 __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, t = lane >> 4;
@@ -597,6 +602,8 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
     const int m = 16 * g + r;
     xoff[g] = m < a.M ? static_cast<unsigned>(m * a.K * 2 + t * 64) : 0x80000000u;
   }
+  // ONE: lane r < 4 of the last group loads piece r of row M - 1 (16 * (G - 1))
+  const unsigned xone = r < 4 ? static_cast<unsigned>((16 * (G - 1)) * a.K * 2 + t * 64 + r * 16) : 0x80000000u;
   f32x4 acc[1][G];
   float tot[G][4];
 #pragma unroll
@@ -620,11 +627,17 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
     const size_t so = a.raw ? blk * 128 + slot * 2 : blk * kTileBytesFp4 + 1024 + slot * 2;
     wsc[j] = static_cast<uint16_t>(__builtin_amdgcn_raw_buffer_load_b16(srs, static_cast<int>(so | aoob | o), 0, 0));
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int g = 0; g < G; ++g) {
+      if (ONE && g == G - 1) {
+        xr[j][g][0] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xone | o), cl * 256, 0));
+        continue;
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s)
         xr[j][g][s] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrs, static_cast<int>(xoff[g] | o), cl * 256 + s * 16, 0));
+    }
   };
   static_for<D>([&](auto J) { issue(J, J); });
   for (int c0 = 0; c0 < a.C; c0 += D) {
@@ -638,9 +651,22 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
       R.sc[0] = wsc[j];
       u32x4 xb[G][4];
 #pragma unroll
-      for (int g = 0; g < G; ++g)
+      for (int g = 0; g < G; ++g) {
+        if (ONE && g == G - 1) {
+          // piece s from lane r + s of the 16-lane row (row_shl:s; lanes past the row read 0)
+          const u32x4 v = xr[j][g][0];
+          xb[g][0] = v;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            xb[g][1][q] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v[q]), 0x101, 0xf, 0xf, true));
+            xb[g][2][q] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v[q]), 0x102, 0xf, 0xf, true));
+            xb[g][3][q] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v[q]), 0x103, 0xf, 0xf, true));
+          }
+          continue;
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) xb[g][s] = xr[j][g][s];
+      }
       issue(J, c + D);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -675,6 +701,14 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
     for (int v = 0; v < 4; ++v) val[g][v] = (tot[g][v] * a.scale2) * xi;
   }
   store(val);
+}
+
+template <int G>
+void launch_gather(int M, dim3 grid, dim3 blk, hipStream_t s, const GatherArgs& a) {
+  if (M % 16 == 1)
+    hipLaunchKernelGGL((gather_kernel<G, true>), grid, blk, 0, s, a);
+  else
+    hipLaunchKernelGGL((gather_kernel<G, false>), grid, blk, 0, s, a);
 }
 
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
@@ -1361,11 +1395,11 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (cdiv(M, 16)) {
-    case 1: hipLaunchKernelGGL(gather_kernel<1>, grid, blk, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(gather_kernel<2>, grid, blk, 0, s, a); break;
-    case 3: hipLaunchKernelGGL(gather_kernel<3>, grid, blk, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(gather_kernel<4>, grid, blk, 0, s, a); break;
-    default: hipLaunchKernelGGL(gather_kernel<5>, grid, blk, 0, s, a); break;
+    case 1: launch_gather<1>(M, grid, blk, s, a); break;
+    case 2: launch_gather<2>(M, grid, blk, s, a); break;
+    case 3: launch_gather<3>(M, grid, blk, s, a); break;
+    case 4: launch_gather<4>(M, grid, blk, s, a); break;
+    default: launch_gather<5>(M, grid, blk, s, a); break;
   }
   return check_launch("stream_gemm_gather");
 }

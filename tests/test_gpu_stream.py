@@ -311,7 +311,7 @@ def test_stream_gemm_gather_nvfp4_bit_exact(L, N, K):
     cap = (cnt + 96 + 31) // 32 * 32
     drows = to_dev(rows)
     x = O.normal_f32(61, 1.0, (68, K))
-    for M in [1, 11, 17, 68]:
+    for M in [1, 11, 17, 33, 65, 68]:
         xh, xinv = L.to_half_rows(to_dev(x[:M]))
         full = L.stream_gemm_nvfp4(xh, xinv, raw, None, g, N, K).cpu().numpy()
         for c in [cnt, 5, 0]:
