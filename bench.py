@@ -176,6 +176,11 @@ def bench_verify_mlp(torch, L, O, args, dev):
         wg, sg, wu, su, _, _ = sets[i % copies]
         L.stream_fp8_pc_silu_mul(x, wg, sg, wu, su, F, h=h)
     gu_b2b = timed(gu_only)
+
+    def dn_only(i):
+        _, _, _, _, wd, sd = sets[i % copies]
+        L.stream_fp8_pc_residual(h, wd, sd, r, H, y=r)
+    dn_b2b = timed(dn_only)
     # algorithmic bytes: weights + scales + activations in/out (+ residual read and write); h counted as the
     # gate|up output and the down input
     b_gu = 2 * F * H + 2 * F * 4 + M * H * 2 + M * F * 2
@@ -189,7 +194,8 @@ def bench_verify_mlp(torch, L, O, args, dev):
         "one_launch": {"ms": ms1, "gb_s": (b_gu + b_dn) / (ms1 * 1e-3) / 1e9},
         "gate_up": {"ms": gu_b2b, "bytes": b_gu, "gb_s": b_gu / (gu_b2b * 1e-3) / 1e9,
                     "ms_event_pair": gu_ms, "gb_s_event_pair": b_gu / (gu_ms * 1e-3) / 1e9},
-        "down": {"ms": dn_ms, "bytes": b_dn, "gb_s": b_dn / (dn_ms * 1e-3) / 1e9},
+        "down": {"ms": dn_b2b, "bytes": b_dn, "gb_s": b_dn / (dn_b2b * 1e-3) / 1e9,
+                 "ms_event_pair": dn_ms, "gb_s_event_pair": b_dn / (dn_ms * 1e-3) / 1e9},
         "rotation_copies": copies,
         "deadline_hit": L.stream_ffn_deadline_status(),
     }
@@ -287,7 +293,7 @@ def bench_decode_step(torch, L, O, args, dev):
                 r = out(N)
                 L.stream_fp8_pc_residual(xs[K], ws[0][0], ws[0][1], r, N, y=r)
 
-    steps = max(1, min(args.steps // 20, 10))
+    steps = max(3, min(args.steps // 20, 10))
     step()
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -442,15 +448,22 @@ def cpu_baseline(O):
         dt = time.perf_counter() - t
         best = dt if best is None else min(best, dt)
     b = (2 * F * H + 2 * F * 4 + M * H * 2 + M * F * 2) + (H * F + H * 4 + M * F * 2 + 2 * M * H * 2)
-    cpu = "unknown"
+    # the model string, with the family / model / stepping numbers (a virtual machine's model string can be generic)
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for ln in f:
-                if ln.startswith("model name"):
-                    cpu = ln.split(":", 1)[1].strip()
+                k, _, v = ln.partition(":")
+                k = k.strip()
+                if k in ("model name", "cpu family", "model", "stepping") and k not in info:
+                    info[k] = v.strip()
+                if not ln.strip() and info:
                     break
     except OSError:
         pass
+    cpu = info.get("model name", "unknown")
+    if "cpu family" in info:
+        cpu += f" (family {info['cpu family']}, model {info.get('model', '?')}, stepping {info.get('stepping', '?')})
     return {"value": round(b / best / 1e9, 3), "unit": "GB/s", "cores": threads, "cpu": cpu, "kind": "port",
             "sample": f"one full verify-MLP pass (M=17; gate and up 5120->17408, down 17408->5120; FP8 per-channel) "
                       f"through the oracle's C path, best of 3: {best:.2f} s per pass, "

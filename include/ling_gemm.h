@@ -134,9 +134,9 @@ int lq_stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* ws
                      void* stream);
 /* The same computation with no allocation of any kind: no counterpart in the reference; for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Its split-K partial
- * sums and arrival counters live in a fixed 20 MiB + 256 KiB device array of the library (one per GPU, held until
- * the process ends) instead of the workspace: launches needing more (more than 256 workgroups' partials, or more
- * than 65536 tile groups) fail with LQ_ERR_SHAPE before anything runs. Results equal lq_stream_fp8_pc's bit for
+ * sums and arrival counters live in a fixed 25 MiB + 256 KiB device array of the library (one per GPU, held until
+ * the process ends) instead of the workspace: enough for any M <= 80 on devices of up to 320 CUs; launches needing
+ * more (more than 320 workgroups' partials, or more than 65536 tile groups) fail with LQ_ERR_SHAPE before anything runs. Results equal lq_stream_fp8_pc's bit for
  * bit. All calls on one GPU share the array: calls that overlap on one GPU (two streams) race, so serialize them.
  * Call lq_init first when the first call may be graph-captured (it clears the array's counters eagerly). */
 int lq_stream_fp8_pc_noalloc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N,

@@ -14,7 +14,9 @@ float e4m3_decode(uint8_t c);
 float bf16_to_f32(uint16_t b);
 uint16_t f32_to_bf16(float x);  // round to nearest even
 float f16_to_f32(uint16_t h);
-// element i of a [N][K] weight of type dtype (LQ_DT_*) as FP32 (exact)
+// element i of a [N][K] weight of type dtype (LQ_DT_*) as FP32 (exact); dtype | kRoundBf16: the element rounded
+// to BF16 (nearest even) on the fly, so a caller needs no BF16 copy of an F16 / F32 weight
+constexpr int kRoundBf16 = 0x100;
 float element(const void* w, int dtype, size_t i);
 
 // NVFP4 round-to-nearest in two passes: the global scale g (returned) and the E4M3 block scales [N][K/16]; then

@@ -79,6 +79,7 @@ float f16_to_f32(uint16_t h) {
 }
 
 float element(const void* w, int dtype, size_t i) {
+  if (dtype & kRoundBf16) return bf16_to_f32(f32_to_bf16(element(w, dtype & ~kRoundBf16, i)));
   switch (dtype) {
     case LQ_DT_BF16: return bf16_to_f32(static_cast<const uint16_t*>(w)[i]);
     case LQ_DT_F16: return f16_to_f32(static_cast<const uint16_t*>(w)[i]);

@@ -563,7 +563,10 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
 
   // every streaming workgroup of tg has published and counted itself (one wave polls, about every half
   // microsecond: the polls of all finish workgroups land on a few cache lines)
-  if (wave == 0) {
+  if (wave == 0 && a.wait_ms == 0) {
+    // zero limit (a test hook): give up at once, so the expired-wait path below is taken on every launch
+    __hip_atomic_store(&g_wait_expired, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if (wave == 0) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
     while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg, __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_AGENT)) < n) {

@@ -1183,11 +1183,11 @@ __global__ void __launch_bounds__(256) zero_ints_kernel(int* p, int n) {
 
 // ---------------- the no-allocation entry point's scratch ----------------
 // lq_stream_fp8_pc_noalloc keeps its split-K partial sums and arrival counters in this file-scope device array
-// instead of the library's workspace: 20 MiB of partials (two slots per workgroup at 256 workgroups, two tiles per
-// wave and five row groups: M <= 80) and 64 Ki counters. Every GPU the library runs on holds its own copy until the
+// instead of the library's workspace: 25 MiB of partials (two slots per workgroup at up to 320 workgroups, one per CU,
+// two tiles per wave and five row groups: M <= 80, on devices of up to 320 CUs) and 64 Ki counters. Every GPU the library runs on holds its own copy until the
 // process ends. Host code never passes the array's name to a kernel (on the host it is only a stand-in): its
 // device address is looked up once per device (noalloc_scratch) and that address is used.
-constexpr size_t kScratchPartialBytes = size_t(20) << 20;
+constexpr size_t kScratchPartialBytes = size_t(25) << 20;  // 2 x 320 x 40 KiB
 constexpr size_t kScratchCounters = size_t(1) << 16;
 static __device__ __align__(256) unsigned char scratch[kScratchPartialBytes + 4 * kScratchCounters];
 
@@ -1240,8 +1240,8 @@ using namespace lq;
 extern "C" {
 
 // Test hook (not part of the interface): the finish workgroups' wait limit for later launches, in milliseconds
-// (default 1000; 0 makes a wait give up at its first unanswered poll, so tests can reach the expired-wait path
-// without a stalled GPU). Returns the previous limit, or -1 for a value outside [0, 32767].
+// (default 1000; 0 makes every finish workgroup give up without waiting, so tests reach the expired-wait path
+// deterministically without a stalled GPU). Returns the previous limit, or -1 for a value outside [0, 32767].
 int lq_debug_finish_wait_ms(int ms) {
   if (ms < 0 || ms > 32767) return -1;
   return g_finish_wait_ms.exchange(ms);
@@ -1369,8 +1369,10 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
     return fail(LQ_ERR_SHAPE, nm + ": K % 128 and cap % 32 must be 0");
   if (M < 1 || M > LQ_MAX_STREAM_ROWS) return fail(LQ_ERR_SHAPE, nm + ": M must be in [1, 80]");
   if (N <= 0 || N % 16 != 0) return fail(LQ_ERR_SHAPE, nm + ": N % 16 and K % 128 must be 0");
-  if (static_cast<long long>(N / 16) * (K / kChunk) * kTileBytesFp4 >= (1LL << 31))
-    return fail(LQ_ERR_SHAPE, nm + ": weight blob must be below 2^31 bytes");
+  // the kernel addresses the blob and the activations with 32-bit byte offsets (bit 31 marks a read out of range)
+  if (static_cast<long long>(N / 16) * (K / kChunk) * kTileBytesFp4 >= (1LL << 31) ||
+      static_cast<long long>(M) * K * 2 >= (1LL << 31))
+    return fail(LQ_ERR_SHAPE, nm + ": weight blob and activations must be below 2^31 bytes");
   if (!xh || !xinv || !w || !rows || !nrows || !y) return fail(LQ_ERR_ARG, nm + ": null pointer");
   GatherArgs a{};
   a.x = xh;

@@ -585,7 +585,7 @@ constexpr int kQuantFlags = LQ_WFILE_QUANT_FP8 | LQ_WFILE_QUANT_FP8_BLOCK | LQ_W
 
 // A high-precision linear weight quantized here (LQ_WFILE_QUANT_*): a 2-D P.weight in BF16, F16 or F32 with no
 // scale tensors of its own, N % 16 == 0 and K % 128 == 0, and a name naming neither an embedding nor a norm (those
-// are lookups and vectors, not GEMM operands). Anything else is left to the passthrough. NVFP4 takes BF16 values
+// are lookups and vectors, not GEMM operands) nor a MoE router. Anything else is left to the passthrough. NVFP4 takes BF16 values
 // (the reference's quantize_nvfp4, src/core/model.cu:188-249, rounds BF16): F16 and F32 weights are rounded to
 // BF16 first. FP8 quantizes the exact FP32 values.
 void plan_quantized(const Checkpoint& ck, const std::string& name, const std::string& prefix, const Tensor& w,
@@ -597,6 +597,13 @@ void plan_quantized(const Checkpoint& ck, const std::string& name, const std::st
   else return;
   if (w.shape.size() != 2 || ck.find(prefix + ".weight_scale") || ck.find(prefix + ".weight_scale_inv")) return;
   if (name.find("embed") != std::string::npos || name.find("norm") != std::string::npos) return;
+  // MoE routers (P = "....gate" or a name with "router") stay in their own precision: their outputs pick the
+  // experts, and the reference quantizes only the projections it streams (src/core/drafter.cpp:93-100)
+  const std::string gate_suffix = ".gate";
+  if (prefix.find("router") != std::string::npos ||
+      (prefix.size() >= gate_suffix.size() &&
+       prefix.compare(prefix.size() - gate_suffix.size(), gate_suffix.size(), gate_suffix) == 0))
+    return;
   if (w.shape[0] <= 0 || w.shape[1] <= 0 || w.shape[0] > (int64_t(1) << 30) || w.shape[1] > (int64_t(1) << 29)) return;
   const int N = static_cast<int>(w.shape[0]), K = static_cast<int>(w.shape[1]);
   if (N % 16 != 0 || K % kChunk != 0) return;
@@ -619,19 +626,19 @@ void plan_quantized(const Checkpoint& ck, const std::string& name, const std::st
   consumed.insert(name);
   const uint8_t* src = w.data;
   if (flags & LQ_WFILE_QUANT_NVFP4) {
-    // BF16 values (rounded once here for F16 / F32), then the scales now: whether the blob is coded depends on them
-    auto bf = std::make_shared<std::vector<uint16_t>>();
-    const void* vals = src;
-    if (dt != LQ_DT_BF16) {
-      bf->resize(size_t(N) * K);
-      for (size_t i = 0; i < bf->size(); ++i) (*bf)[i] = lq::hostq::f32_to_bf16(lq::hostq::element(src, dt, i));
-      vals = bf->data();
-    }
-    auto scl = std::make_shared<std::vector<uint8_t>>(size_t(N) * K / 16);
-    const float g = lq::hostq::nvfp4_scales(vals, LQ_DT_BF16, N, K, scl->data());
-    e.weight_scale = g;
+    // BF16 values: F16 / F32 elements are rounded to BF16 as they are read, so no copy of the weight is made. The
+    // block scales decide here whether the blob is coded, and are made again when the entry is filled: a plan keeps
+    // only its 64-byte code table, so planning a whole checkpoint holds no per-weight buffers.
+    const int vdt = dt == LQ_DT_BF16 ? dt : (dt | lq::hostq::kRoundBf16);
+    float g;
     uint8_t table[64], code_of[256];
-    const bool coded = !(flags & LQ_WFILE_NO_CODES) && lq_scale_code_table(scl->data(), scl->size(), table, code_of) == 1;
+    bool coded;
+    {
+      std::vector<uint8_t> scl(size_t(N) * K / 16);
+      g = lq::hostq::nvfp4_scales(src, vdt, N, K, scl.data());
+      coded = !(flags & LQ_WFILE_NO_CODES) && lq_scale_code_table(scl.data(), scl.size(), table, code_of) == 1;
+    }
+    e.weight_scale = g;
     if (coded) {
       e.kind = LQ_WENTRY_NVFP4_CODED;
       e.blob_bytes = lq_tiled_bytes_nvfp4_coded(N, K);
@@ -643,14 +650,14 @@ void plan_quantized(const Checkpoint& ck, const std::string& name, const std::st
     }
     std::vector<uint8_t> tab(table, table + 64), map(code_of, code_of + 256);
     p.fill = [=](uint8_t* blob, uint8_t* aux, uint8_t* tb) {
-      std::vector<uint8_t> v(size_t(N) * K / 2);
-      (void)lq::hostq::nvfp4_values(vals, LQ_DT_BF16, N, K, g, scl->data(), v.data());
-      (void)bf;  // keeps the BF16 copy alive until the values are made
+      std::vector<uint8_t> scl(size_t(N) * K / 16), v(size_t(N) * K / 2);
+      (void)lq::hostq::nvfp4_scales(src, vdt, N, K, scl.data());
+      (void)lq::hostq::nvfp4_values(src, vdt, N, K, g, scl.data(), v.data());
       if (coded) {
-        host_retile_nvfp4_coded(v.data(), scl->data(), map.data(), blob, aux, N, K);
+        host_retile_nvfp4_coded(v.data(), scl.data(), map.data(), blob, aux, N, K);
         std::memcpy(tb, tab.data(), 64);
       } else {
-        host_retile_nvfp4_values(v.data(), scl->data(), blob, 1152, nullptr, N, K);
+        host_retile_nvfp4_values(v.data(), scl.data(), blob, 1152, nullptr, N, K);
       }
     };
   } else {

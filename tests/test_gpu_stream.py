@@ -376,6 +376,10 @@ def test_error_paths(L):
     rc = L.lib.lq_stream_gemm_gather_nvfp4(x.data_ptr(), yg.data_ptr(), 1, tw.data_ptr(), None, 1.0, rows.data_ptr(),
                                            rows.data_ptr(), 32, yg.data_ptr(), 16384, 262144, None)
     assert rc != 0 and b"2^31" in L.lib.lq_last_error()
+    # activations of 2 GiB or more (M = 80, K = 104858 chunks) with a small weight blob (N = 16) are refused too
+    rc = L.lib.lq_stream_gemm_gather_nvfp4(x.data_ptr(), yg.data_ptr(), 80, tw.data_ptr(), None, 1.0, rows.data_ptr(),
+                                           rows.data_ptr(), 32, yg.data_ptr(), 104858 * 128, 16, None)
+    assert rc != 0 and b"2^31" in L.lib.lq_last_error()
 
 
 def test_caller_workspace(L):
@@ -508,7 +512,8 @@ def test_expired_finish_wait_leaves_counters_consistent(L):
         torch.cuda.synchronize()
     finally:
         assert hook(prev) == 0
-    print(f"expired finish waits reported: {L.stream_ffn_deadline_status()}", flush=True)
+    # a zero limit makes every finish workgroup give up without waiting: the expiry is always reported
+    assert L.stream_ffn_deadline_status() == 1
     assert L.stream_ffn_deadline_status() == 0  # reading cleared the flag
     for _ in range(3):
         got = L.stream_gemm_fp8(xh, xinv, w, 0.5, N, K).view(torch.int32).cpu().numpy()

@@ -140,6 +140,15 @@ def test_fp8_block_quantizers_reconstruct():
         for kb in range(3):
             blk = q[nb * 128:(nb + 1) * 128, kb * 128:(kb + 1) * 128]
             assert (blk & 0x7F).max() == 0x7E
+    # scales and codes byte for byte against torch: s = amax / 448 per 128 x 128 block, codes = float8_e4m3fn of
+    # w / s (FP32 division, clamped to +-448)
+    import torch
+    wt = torch.from_numpy(w)
+    blocks = wt.view(2, 128, 3, 128)
+    st = blocks.abs().amax(dim=(1, 3)) / 448.0
+    assert np.array_equal(s, st.numpy())
+    qt = (blocks / st[:, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn).view(torch.uint8).view(256, 384)
+    assert np.array_equal(q, qt.numpy())
     x = O.normal_bf16(10, 1.0, (4, 256))
     xq, xs = O.quant_act_fp8_g128(x)
     xf = O.bf16_to_f32(x)

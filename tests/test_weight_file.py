@@ -339,18 +339,23 @@ def test_compile_quantizes_high_precision_linears(tmp_path):
     wf = O.normal_f32(42, 0.02, (32, 384))
     emb = O.normal_bf16(43, 0.02, (64, 256))
     odd = O.normal_bf16(44, 0.02, (24, 256))  # N % 16 != 0
+    router = O.normal_bf16(45, 0.02, (32, 256))  # MoE router gates (N = #experts) stay as they are
     _single(d, {"m.q_proj.weight": ("BF16", wb.shape, wb), "m.o_proj.weight": ("F32", wf.shape, wf),
+                "m.mlp.gate.weight": ("BF16", router.shape, router), "m.mlp.router.weight": ("BF16", router.shape, router),
+                "m.mlp.gate_proj.weight": ("BF16", wb.shape, wb),
                 "m.o_proj.input_scale": ("F32", [], np.float32([0.5])),
                 "m.embed_tokens.weight": ("BF16", emb.shape, emb), "m.odd.weight": ("BF16", odd.shape, odd),
                 "m.post_norm.weight": ("BF16", (256,), wb[0])})
     for mode in ("fp8", "fp8-block", "nvfp4"):
         out = str(tmp_path / f"{mode}.lqw")
         n = LC.compile_checkpoint(d, out, quantize=mode, passthrough=True)
-        assert n == 5
+        assert n == 8
         with LC.WeightFile(out) as f:
             assert {f.entry(i).name for i in range(len(f))} == {"m.q_proj", "m.o_proj", "m.embed_tokens.weight",
-                                                                 "m.odd.weight", "m.post_norm.weight"}
-            for name, src, dt in (("m.q_proj", wb, "BF16"), ("m.o_proj", wf, "F32")):
+                                                                 "m.odd.weight", "m.post_norm.weight",
+                                                                 "m.mlp.gate.weight", "m.mlp.router.weight",
+                                                                 "m.mlp.gate_proj"}
+            for name, src, dt in (("m.q_proj", wb, "BF16"), ("m.o_proj", wf, "F32"), ("m.mlp.gate_proj", wb, "BF16")):
                 e = f.entry(name)
                 f.verify(name)
                 assert e.quantized and e.dtype == dt
@@ -372,7 +377,8 @@ def test_compile_quantizes_high_precision_linears(tmp_path):
                     assert np.array_equal(e.blob, O.retile_fp8(q))
                     assert np.array_equal(e.aux.view(np.float32), s.reshape(-1))
             assert f.entry("m.o_proj").input_scale == 0.5
-            for raw in ("m.embed_tokens.weight", "m.odd.weight", "m.post_norm.weight"):
+            for raw in ("m.embed_tokens.weight", "m.odd.weight", "m.post_norm.weight", "m.mlp.gate.weight",
+                        "m.mlp.router.weight"):
                 assert f.entry(raw).kind == L.WENTRY_RAW
     with pytest.raises(L.LingGemmError, match="at most one"):
         L._check(L.lib.lq_wfile_compile(d.encode(), str(tmp_path / "x.lqw").encode(),

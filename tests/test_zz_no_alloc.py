@@ -36,7 +36,7 @@ def _noalloc(L, x, tw, s, N, K):
 
 
 def test_noalloc_equals_workspace_entry_point(L):
-    # (68, 5120, 17408): finish workgroups do the split-K sums, with the partials filling the fixed scratch exactly
+    # (68, 5120, 17408): finish workgroups do the split-K sums, with the partials filling 20 of the fixed scratch's 25 MiB
     cases = [(68, 5120, 17408, 500), (68, 17408, 5120, 501), (17, 5120, 17408, 502), (1, 5120, 5120, 503),
              (5, 1024, 1024, 504)]
     for M, N, K, seed in cases:  # each call after the first uses a smaller input than the one before
