@@ -463,7 +463,7 @@ def cpu_baseline(O):
         pass
     cpu = info.get("model name", "unknown")
     if "cpu family" in info:
-        cpu += f" (family {info['cpu family']}, model {info.get('model', '?')}, stepping {info.get('stepping', '?')})
+        cpu += f" (family {info['cpu family']}, model {info.get('model', '?')}, stepping {info.get('stepping', '?')})"
     return {"value": round(b / best / 1e9, 3), "unit": "GB/s", "cores": threads, "cpu": cpu, "kind": "port",
             "sample": f"one full verify-MLP pass (M=17; gate and up 5120->17408, down 17408->5120; FP8 per-channel) "
                       f"through the oracle's C path, best of 3: {best:.2f} s per pass, "

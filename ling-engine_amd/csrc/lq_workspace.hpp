@@ -16,7 +16,7 @@ struct Workspace {
   size_t counter_count = 0;
   int* sync = nullptr;
   bool external = false;  // partials, counters and sync live in a caller-owned buffer (lq_set_workspace)
-  // sync[16]: the one-launch FFN's phase-A arrivals, exits, deadline flag (zeroed once, self-resetting)
+  // sync[64]: the one-launch FFN's phase-A arrivals, exits, deadline flag, ready flag at [32] (zeroed once, self-resetting)
   // prefill tail split: FP32 partial tiles and per-tile arrival counters (zeroed once, self-resetting)
   float* pf_partials = nullptr;
   size_t pf_partial_bytes = 0;

@@ -79,7 +79,7 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
     counter_count = cap;
   }
   if (!sync) {
-    if (hipMalloc(&sync, 16 * sizeof(int)) != hipSuccess || hipMemset(sync, 0, 16 * sizeof(int)) != hipSuccess) {
+    if (hipMalloc(&sync, 64 * sizeof(int)) != hipSuccess || hipMemset(sync, 0, 64 * sizeof(int)) != hipSuccess) {
       sync = nullptr;
       return fail(LQ_ERR_DEVICE, "workspace: counter allocation failed");
     }

@@ -45,8 +45,11 @@
 
 namespace lq {
 namespace {
-template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, int MODE, class Ready>
-__device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>& sm, Ready&& ready) {
+// NPRE (with kXCoh only): the range's first NPRE chunks run ahead (see the prologue), with their activation images and
+// wave 0's weights in xpre.
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, int MODE, int NPRE = 0, class Ready>
+__device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>& sm, Ready&& ready,
+                                            uint8_t* xpre = nullptr) {
   constexpr int T = TW;
   constexpr int PF = pf_stages<T>(G);
   constexpr bool BPRE = Smem<G>::BPRE;
@@ -56,6 +59,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   constexpr bool CVT = (MODE & kCvt) != 0;
   static_assert(!CVT || F16, "converted activations feed the FP16 MFMA");
   static_assert(!BPRE || PF >= 3, "the operand prefetch needs a chunk of lookahead");
+  static_assert(NPRE == 0 || (XCOH && !CVT), "run-ahead chunks are for the activation-waiting form");
+  constexpr int NP1 = NPRE > 0 ? NPRE : 1;
   auto& xs = sm.xs;
   auto& tabs = sm.tabs;
   auto& last_flag = sm.last_flag;
@@ -254,8 +259,87 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   epi_load<G, PAIR, OUTF32, T>(a, sL.mi, sL.wtile0, eL, r, t);
   LQ_TS(13);
 
-  const int npad = (n_it + PF - 1) / PF * PF;
-  if constexpr (XCOH) {
+  // the ring streams the chunks after the NPRE run-ahead ones (n_ring of them)
+  const int n_ring = max(n_it - NPRE, 0);
+  const int npad = (n_ring + PF - 1) / PF * PF;
+  WRegs<WF, T> pr[NP1];
+  if constexpr (XCOH && NPRE > 0) {
+    // Run-ahead: before the wait for the activations, waves 1-3 load the weights of the range's first NPRE chunks and
+    // of the ring's first stages into registers. Wave 0 issues no load before the wait, so that its polls in ready()
+    // return at the memory's latency (a poll's result waits for every load the wave issued before it), and loads its
+    // share right after. Then the run-ahead chunks' activation images come straight into LDS, the ring's activations
+    // follow, and the run-ahead chunks are computed while the ring's loads are in flight.
+    static_assert(WF == kFp8, "the run-ahead form streams FP8 weights");
+    int plc[NP1];
+    unsigned poob[NP1];
+    SegTiles<WF, T, PAIR> Lp[NP1];
+#pragma unroll
+    for (int c = 0; c < NPRE; ++c) {
+      poob[c] = lleft > 0 ? 0u : 0x80000000u;
+      plc[c] = lc;
+      Lp[c] = L;
+      if (wave != 0) load_w<WF, T>(pr[c], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | poob[c]), slot, poob[c]);
+      advance();
+    }
+    int lcs[PF - 1];
+    unsigned oobs[PF - 1];
+    SegTiles<WF, T, PAIR> Lr[PF - 1];
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) {
+      oobs[j] = lleft > 0 ? 0u : 0x80000000u;
+      lcs[j] = lc;
+      Lr[j] = L;
+      if (wave != 0) load_w<WF, T>(wr[j], L.rs, L.toff, L.coff, lc, static_cast<int>(lane_off | oobs[j]), slot, oobs[j]);
+      advance();
+    }
+    ready();
+    LQ_TS(15);
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < NPRE; ++c)
+        load_w<WF, T>(pr[c], Lp[c].rs, Lp[c].toff, Lp[c].coff, plc[c], static_cast<int>(lane_off | poob[c]), slot,
+                      poob[c]);
+    }
+    // chunk c's image: 16G rows x 16 units of 16 bytes, as put_x lays it out (unit u of row m at u ^ (m & 15));
+    // load k of wave w fills 64 consecutive units (rows 4 (4k + w) .. +4), each lane fetching the source unit that
+    // belongs at its place
+#pragma unroll
+    for (int c = 0; c < NPRE; ++c)
+#pragma unroll
+      for (int k = 0; k < G; ++k) {
+        const int row = 4 * (4 * k + wave) + (lane >> 4), u = (lane & 15) ^ (row & 15);
+        const unsigned src = row < a.M ? static_cast<unsigned>((row * a.K) * 2 + u * 16) : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xrs, (__attribute__((address_space(3))) void*)(xpre + c * Smem<G>::XS_BYTES + (4 * k + wave) * 1024), 16,
+            static_cast<int>(src | poob[c]), __builtin_amdgcn_readfirstlane(plc[c] * 256), 0, XPOL);
+      }
+    if (wave == 0) {
+#pragma unroll
+      for (int j = 0; j < PF - 1; ++j)
+        load_w<WF, T>(wr[j], Lr[j].rs, Lr[j].toff, Lr[j].coff, lcs[j], static_cast<int>(lane_off | oobs[j]), slot,
+                      oobs[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < PF - 1; ++j) load_x(j, lcs[j], oobs[j]);
+    // the run-ahead images have landed (only the ring's loads, issued after them, may still be in flight)
+    constexpr int kLater = (PF - 1) * G, kLater0 = (PF - 1) * (G + 2 * T);
+    static_assert(kLater0 < 64, "vmcnt holds at most 63");
+    if (wave == 0)
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (kLater0 & 15) | ((kLater0 >> 4) << 14));
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70 | (kLater & 15) | ((kLater >> 4) << 14));
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NPRE; ++c) {
+      if (c < n_it) {
+        const uint8_t* tab[T];
+        tables(tab);
+        compute_lds<WF, F16, G, T>(pr[c], xpre + c * Smem<G>::XS_BYTES, acc2, r, t, tab);
+        if (c == 0) LQ_TS(1);
+        after_chunk(c);
+      }
+    }
+  } else if constexpr (XCOH) {
     // weights of the first stages first, then the wait for the activations, then their loads
     int lcs[PF - 1];
     unsigned oobs[PF - 1];
@@ -298,7 +382,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
 #pragma unroll
         for (int s = 0; s < 4; ++s) read_b<G>(bn[s], xs[sl], s, r, t);
         if constexpr (CVT) chunk_scales(scn, sl);
-        if (it < n_it) {
+        if (it < n_ring) {
           const uint8_t* tab[T];
           tables(tab);
           if constexpr (CVT) {
@@ -310,8 +394,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
 #pragma unroll
             for (int s = 0; s < 4; ++s) mfma_step<WF, F16, G, T>(wr[j], s, bc[s], acc2, tab);
           }
-          if (it == 0) LQ_TS(1);
-          after_chunk(it);
+          if (NPRE == 0 && it == 0) LQ_TS(1);
+          after_chunk(NPRE + it);
         }
 #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -332,7 +416,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
         load_stage_x((j + PF - 1) % PF);
         __syncthreads();
         load_stage_w((j + PF - 1) % PF);
-        if (it < n_it) {
+        if (it < n_ring) {
           const uint8_t* tab[T];
           tables(tab);
           if constexpr (CVT) {
@@ -344,8 +428,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
           } else {
             compute_lds<WF, F16, G, T>(wr[j], xs[it & 1], acc2, r, t, tab);
           }
-          if (it == 0) LQ_TS(1);
-          after_chunk(it);
+          if (NPRE == 0 && it == 0) LQ_TS(1);
+          after_chunk(NPRE + it);
         }
       }
     }
@@ -459,10 +543,20 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
 // this kernel per device at a time); a wait past its deadline records sync[2] = 1 and goes on, so the
 // kernel always exits. The last workgroup out resets the counters (no memset node in a captured graph).
 constexpr unsigned long long kFfnDeadlineTicks = 10'000'000ull;  // s_memrealtime at 100 MHz: 100 ms
+constexpr int kFfnFlag = 32;  // sync[32]: phase B may read h (128 bytes past the counters)
+
+#ifndef LQ_NPRE2
+#define LQ_NPRE2 4
+#endif
+// Phase B's run-ahead chunks (weights in registers, their activation images in LDS), by register budget.
+template <int G>
+constexpr int ffn_run_ahead() { return LQ_NPRE2; }
 
 template <int G>
 __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const StreamArgs b, int* sync) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
+  constexpr int NPRE = ffn_run_ahead<G>();
+  __shared__ __attribute__((aligned(16))) uint8_t xpre[(NPRE > 0 ? NPRE : 1) * Smem<G>::XS_BYTES];  // run-ahead activation images
   const int p = logical_wg<true>(a);  // (both phases are one segment of the same P workgroups)
   stream_body<G, kFp8, 2, false, true, false, kYCoh>(a, p, sm, NoWait{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's h stores have completed
@@ -472,13 +566,16 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
   // caches (sc1) only after it has seen all P arrivals. So no cache needs a writeback or an invalidation: a release
   // / acquire pair at agent scope adds an L2 writeback to each arrival and an L2 invalidation to each poll, which
   // measured 10 us slower per step than these relaxed atomics.
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // The last to arrive raises the ready flag (sync[kFfnFlag], a cache line of its own): the pollers read the flag, so
+  // that their reads do not queue with the arrivals' atomics on the counter.
   const int P = a.P;
+  if (threadIdx.x == 0 && __hip_atomic_fetch_add(sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1)
+    __hip_atomic_store(sync + kFfnFlag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   auto ready = [&]() {
     if (threadIdx.x == 0) {
       const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-      while (__hip_atomic_load(sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < P) {
-        __builtin_amdgcn_s_sleep(2);
+      while (__hip_atomic_load(sync + kFfnFlag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) {
+        __builtin_amdgcn_s_sleep(8);
         if (__builtin_amdgcn_s_memrealtime() - t0 > kFfnDeadlineTicks) {
           __hip_atomic_store(sync + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           break;
@@ -487,12 +584,13 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
     }
     __syncthreads();
   };
-  stream_body<G, kFp8, 2, false, false, false, kXCoh>(b, p, sm, ready);
+  stream_body<G, kFp8, 2, false, false, false, kXCoh, NPRE>(b, p, sm, ready, xpre);
   __syncthreads();
   if (threadIdx.x == 0 &&
       __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1) {
     __hip_atomic_store(sync, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_store(sync + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sync + kFfnFlag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1106,7 +1204,7 @@ int ffn_launch(const char* name, const uint16_t* x, int M, const Mat (&gu)[2], c
   if (rc) return rc;
   rc = stream_args(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, b);
   if (rc) return rc;
-  if (a.P != b.P || b.T != 2) {  // (the one-launch form runs its down phase at two tiles per wave)
+  if (a.P != b.P || a.T != 2 || b.T != 2) {  // (the one-launch form runs both phases at two tiles per wave)
     rc = stream_launch(name, kFp8, false, true, false, x, nullptr, M, gu, 2, dn.N, s);
     return rc ? rc : stream_launch(name, kFp8, false, false, false, h, nullptr, M, &dn, 1, gu[0].N, s);
   }
