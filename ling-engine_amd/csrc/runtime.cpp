@@ -69,7 +69,7 @@ int Workspace::reserve_stream(size_t bytes, size_t counters_needed) {
     partial_bytes = cap;
   }
   if (counters_needed > counter_count) {
-    const size_t cap = std::max(counters_needed, size_t(1) << 16);
+    const size_t cap = std::max(counters_needed, size_t(1) << 20);
     if (counters) (void)hipFree(counters);
     counters = nullptr;
     counter_count = 0;
@@ -173,7 +173,7 @@ int lq_init(void) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return lq::fail(LQ_ERR_DEVICE, "lq_init: no current device");
   const size_t bound = lq::stream_partial_bound(static_cast<size_t>(lq::device_cus(dev)), LQ_MAX_STREAM_ROWS);
-  int rc = ws->external ? LQ_OK : ws->reserve_stream(std::max(bound, size_t(64) << 20), size_t(1) << 16);
+  int rc = ws->external ? LQ_OK : ws->reserve_stream(std::max(bound, size_t(64) << 20), size_t(1) << 20);
   if (rc) return rc;
   rc = lq::reserve_prefill_scratch(ws);
   if (rc) return rc;

@@ -45,6 +45,7 @@ struct StreamArgs {
   short NR;           // finish workgroups per split tile group (0: the last workgroup to arrive finishes it)
   short count;        // matrices
   short wait_ms;      // finish workgroups: how long to wait for the arrivals before giving up (milliseconds)
+  short cs;           // counter stride in ints: 32 puts each counter on a 128-byte line of its own
   const uint8_t* w[kMaxMats];
   const uint8_t* table[kMaxMats];   // coded NVFP4: device scale-code table [64]
   const float* svec[kMaxMats];      // per-channel scales [N] or null
@@ -60,7 +61,7 @@ struct StreamArgs {
   int wg0[kMaxMats + 1];
   int ldy[kMaxMats];
   float* partials;  // [2 * P][T * G * 4][256] per workgroup slot
-  int* counters;    // [TG]
+  int* counters;    // [TG] (TG + tg: finish workgroups' own), counter i at counters[i * cs]
   unsigned long long* trace;  // [P][16] s_memrealtime stamps per workgroup (LQ_STREAM_TRACE builds), or null
 };
 
@@ -568,7 +569,7 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
     __hip_atomic_store(&g_wait_expired, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else if (wave == 0) {
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg, __ATOMIC_RELAXED,
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(a.counters + tg * a.cs, __ATOMIC_RELAXED,
                                                              __HIP_MEMORY_SCOPE_AGENT)) < n) {
       if (__builtin_amdgcn_s_memrealtime() - t0 > static_cast<unsigned long long>(a.wait_ms) * 100'000ull) {
         __hip_atomic_store(&g_wait_expired, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -580,12 +581,12 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
   __syncthreads();
   LQ_TS(1);
   if (threadIdx.x == 0) {
-    const int old = __hip_atomic_fetch_add(a.counters + a.TG + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int old = __hip_atomic_fetch_add(a.counters + (a.TG + tg) * a.cs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == kFinishShares - 1) {
       // minus the n arrivals rather than a store of zero: after an expired wait, arrivals still to come bring the
       // counter back to exactly zero instead of leaving a count for the next launch
-      __hip_atomic_fetch_add(a.counters + tg, -n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(a.counters + a.TG + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(a.counters + tg * a.cs, -n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.counters + (a.TG + tg) * a.cs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 

@@ -460,7 +460,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-      oldF = __hip_atomic_fetch_add(a.counters + tg_first, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      oldF = __hip_atomic_fetch_add(a.counters + tg_first * a.cs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (splitL) publish_partial<G, T>(a, p, one ? 0 : 1, accL, r);
   else epilogue<G, PAIR, OUTF32, T, YCOH>(a, sL.mi, sL.wtile0, accL, eL, r, t);
@@ -475,8 +475,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   LQ_TS(3);
   if (a.NR) {  // the finish workgroups add the partials
     if (threadIdx.x == 0) {
-      if (splitF) __hip_atomic_fetch_add(a.counters + tg_first, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (splitL) __hip_atomic_fetch_add(a.counters + tg_last, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (splitF) __hip_atomic_fetch_add(a.counters + tg_first * a.cs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (splitL) __hip_atomic_fetch_add(a.counters + tg_last * a.cs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     flush_trace(p);
     return;
@@ -490,9 +490,9 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     int last = 0;
     if (h ? splitL : splitF) {
       const int old = (!h && early) ? oldF
-                                    : __hip_atomic_fetch_add(a.counters + tg, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                                    : __hip_atomic_fetch_add(a.counters + tg * a.cs, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = old == span;
-      if (last) __hip_atomic_store(a.counters + tg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (last) __hip_atomic_store(a.counters + tg * a.cs, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     last_flag[h ? 1 : 0] = last;
   }
@@ -1132,6 +1132,13 @@ bool finish_wgs(const StreamArgs& a) {
   return a.P >= 3 * a.TG && (a.P / a.TG + 1) * a.T * G >= 48;
 }
 
+// Arrival counters one 128-byte line apart (a stride of 32 ints) when the counter memory holds them that way, else
+// packed: the arrivals of every workgroup land on the counters at about the same time, and atomics on one line are
+// performed one after another (measured: the M = 17 down projection's tail). kOwnCounters: what lq_init reserves in
+// the library's own workspace.
+constexpr size_t kOwnCounters = size_t(1) << 20;
+int counter_stride(size_t n, size_t capacity) { return n * 32 <= capacity ? 32 : 1; }
+
 // A fixed scratch region in place of the workspace (the no-allocation entry point): partials and counters, with
 // their capacities; the launch is rejected when it needs more.
 struct FixedScratch {
@@ -1162,8 +1169,10 @@ int stream_launch(const char* name, int fmt, bool f16, bool pair, bool outf32, c
   if (rc) return rc;
   a.NR = static_cast<short>(finish_wgs(a) ? kFinishShares : 0);
   a.wait_ms = static_cast<short>(g_finish_wait_ms.load(std::memory_order_relaxed));
-  const size_t ncnt = static_cast<size_t>(a.TG) * (a.NR ? 2 : 1);
+  const size_t nc = static_cast<size_t>(a.TG) * (a.NR ? 2 : 1);
   const size_t pbytes = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M) * sizeof(float);
+  a.cs = static_cast<short>(counter_stride(nc, fixed ? fixed->counter_count : kOwnCounters));
+  const size_t ncnt = nc * a.cs;
   if (fixed) {
     if (pbytes > fixed->partial_bytes || ncnt > fixed->counter_count)
       return fail(LQ_ERR_SHAPE, std::string(name) + ": the launch needs " + std::to_string(pbytes) +
@@ -1212,12 +1221,13 @@ int ffn_launch(const char* name, const uint16_t* x, int M, const Mat (&gu)[2], c
   if (!ws) return LQ_ERR_DEVICE;
   const size_t fa = 2 * static_cast<size_t>(a.P) * slot_floats(a.T, M);
   const size_t fb = 2 * static_cast<size_t>(b.P) * slot_floats(b.T, M);
-  rc = ws->reserve_stream((fa + fb) * sizeof(float), static_cast<size_t>(a.TG) + b.TG);
+  a.cs = b.cs = static_cast<short>(counter_stride(static_cast<size_t>(a.TG) + b.TG, ws->external ? ws->counter_count : kOwnCounters));
+  rc = ws->reserve_stream((fa + fb) * sizeof(float), (static_cast<size_t>(a.TG) + b.TG) * a.cs);
   if (rc) return rc;
   a.partials = ws->partials;
   a.counters = ws->counters;
   b.partials = ws->partials + fa;
-  b.counters = ws->counters + a.TG;
+  b.counters = ws->counters + static_cast<size_t>(a.TG) * a.cs;
 #ifdef LQ_STREAM_TRACE
   a.trace = g_trace;
   b.trace = g_trace ? g_trace + 16 * static_cast<size_t>(a.P) : nullptr;
