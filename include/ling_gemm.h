@@ -223,6 +223,19 @@ int lq_quant_act_fp8(const float* x, int M, int K, float input_scale, uint8_t* q
 /* quant_act_fp8 over a BF16 copy x [M][K] (8-byte aligned): the bytes the FP32 values it was rounded from give.
  * kernels.cuh:237 quant_act_fp8_bf16in */
 int lq_quant_act_fp8_bf16in(const uint16_t* x, int M, int K, float input_scale, uint8_t* q, void* stream);
+/* The DeltaNet output norm into FP8 for the out-projection: per row of D = 128 (rows = tokens x heads),
+ * v = bf16(x * rstd * w * silu(z)), rstd = 1 / sqrt(sum(x^2) / 128 + eps), q = E4M3_satfinite(v * (1 / input_scale)).
+ * x, z FP32 [rows][128] (16-byte aligned), w BF16 [128], q [rows][128]. D != 128 is LQ_ERR_SHAPE.
+ * kernels.cuh:205-206 gated_rmsnorm_fp8 */
+int lq_gated_rmsnorm_fp8(const float* x, const float* z, const uint16_t* w, int rows, int D, float eps,
+                         float input_scale, uint8_t* q, void* stream);
+/* The same over BF16 x and z (8-byte aligned). kernels.cuh:244-246 gated_rmsnorm_fp8_bf16 */
+int lq_gated_rmsnorm_fp8_bf16(const uint16_t* x, const uint16_t* z, const uint16_t* w, int rows, int D, float eps,
+                              float input_scale, uint8_t* q, void* stream);
+/* The gated attention output into FP8: q[i] = E4M3_satfinite(bf16(x[i] / (1 + e^-gate[i])) * (1 / input_scale)),
+ * n values (n % 4 == 0; the reference drops a tail of n % 4, here it is LQ_ERR_SHAPE). kernels.cuh:207
+ * sigmoid_mul_fp8 */
+int lq_sigmoid_mul_fp8(const float* x, const float* gate, size_t n, float input_scale, uint8_t* q, void* stream);
 /* y[M][0..N) (FP32, rows ldy apart) = alpha * xq . W^T, or += with accumulate; W tiled FP8. N % 128 == 0,
  * K % 128 == 0; M < 1 does nothing. kernels.cuh:213-214 prefill_gemm_fp8 */
 int lq_prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,

@@ -157,6 +157,18 @@ inline void quant_act_fp8(const float* x, int M, int K, float input_scale, uint8
 inline void quant_act_fp8_bf16in(const uint16_t* x_bf16, int M, int K, float input_scale, uint8_t* q, hipStream_t s) {
   lq_check(lq_quant_act_fp8_bf16in(x_bf16, M, K, input_scale, q, s));
 }
+// DeltaNet / attention FP8 producers (kernels.cuh:205-207, 244-246)
+inline void gated_rmsnorm_fp8(const float* x, const float* z, const uint16_t* w, int rows, int D, float eps,
+                              float input_scale, uint8_t* q, hipStream_t s) {
+  lq_check(lq_gated_rmsnorm_fp8(x, z, w, rows, D, eps, input_scale, q, s));
+}
+inline void gated_rmsnorm_fp8_bf16(const uint16_t* x, const uint16_t* z, const uint16_t* w, int rows, int D, float eps,
+                                   float input_scale, uint8_t* q, hipStream_t s) {
+  lq_check(lq_gated_rmsnorm_fp8_bf16(x, z, w, rows, D, eps, input_scale, q, s));
+}
+inline void sigmoid_mul_fp8(const float* x, const float* gate, size_t n, float input_scale, uint8_t* q, hipStream_t s) {
+  lq_check(lq_sigmoid_mul_fp8(x, gate, n, input_scale, q, s));
+}
 inline void prefill_gemm_fp8(const uint8_t* xq, int M, const uint8_t* w, float alpha, float* y, int ldy, int N, int K,
                              bool accumulate, hipStream_t s) {
   lq_check(lq_prefill_gemm_fp8(xq, M, w, alpha, y, ldy, N, K, accumulate ? 1 : 0, s));

@@ -1,6 +1,7 @@
 // Activation producers of the prefill GEMMs, fused with their quantization (reference
-// src/core/prefill_gemm.cu:378-459, 607-637): the NVFP4 activation quantizer, the same on silu(g) * u, and the
-// Gemma RMSNorm straight into FP8 or NVFP4. Every value is rounded to BF16 first (production's activations are
+// src/core/prefill_gemm.cu:378-494, 607-665): the NVFP4 activation quantizer, the same on silu(g) * u, the
+// Gemma RMSNorm straight into FP8 or NVFP4, the DeltaNet gated output norm and the attention's sigmoid gate into
+// FP8. Every value is rounded to BF16 first (production's activations are
 // BF16), as the reference does.
 //
 // NVFP4 (reference put_nvfp4, prefill_gemm.cu:382-394): per block of 16 consecutive values along K,
@@ -178,6 +179,82 @@ int rmsnorm_quant_any(const char* name, const float* x, const uint16_t* w, void*
   return check_launch(name);
 }
 
+// FP8 E4M3 of four BF16-rounded values times inv_scale, saturating, packed low byte first (reference put_fp8x4,
+// prefill_gemm.cu:396-402).
+__device__ __forceinline__ uint32_t fp8x4(const float (&v)[4], float inv_scale) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) w |= e4m3_sat(v[k] * inv_scale) << (8 * k);
+  return w;
+}
+
+__device__ __forceinline__ f32x4 load4(const float* p, size_t i) { return reinterpret_cast<const f32x4*>(p)[i]; }
+__device__ __forceinline__ f32x4 load4(const uint16_t* p, size_t i) {
+  const u32x2 u = reinterpret_cast<const u32x2*>(p)[i];
+  return f32x4{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
+               __uint_as_float(u[1] & 0xffff0000u)};
+}
+
+// The DeltaNet output norm over heads of D = 128 (reference gated_norm_fp8_kernel, prefill_gemm.cu:461-482):
+// v = BF16(x * rstd * w * silu(z)), q = E4M3_sat(v * inv_scale). One row per half wave (32 lanes, four values
+// each), so a 64-wide wave finishes two rows from two 512-byte FP32 reads per operand. The sum of squares is
+// the reference's order: per lane fma(x3, x3, fma(x2, x2, fma(x1, x1, x0 * x0))), then the xor butterfly over
+// lane distances 16, 8, 4, 2, 1 inside the half wave (every lane ends with the same tree sum);
+// rstd = 1 / sqrt(ss / 128 + eps), both operations rounded correctly.
+template <typename InT>
+__global__ void __launch_bounds__(256) gated_norm_fp8_kernel(const InT* __restrict__ x, const InT* __restrict__ z,
+                                                             const uint16_t* __restrict__ w, size_t rows, float eps,
+                                                             float inv_scale, uint8_t* __restrict__ q) {
+  const size_t r = blockIdx.x * static_cast<size_t>(8) + (threadIdx.x >> 5);
+  if (r >= rows) return;
+  const int lane = threadIdx.x & 31;
+  const f32x4 f = load4(x, r * 32 + lane);
+  const f32x4 g = load4(z, r * 32 + lane);
+  float ss = f[0] * f[0];
+  ss = __builtin_fmaf(f[1], f[1], ss);
+  ss = __builtin_fmaf(f[2], f[2], ss);
+  ss = __builtin_fmaf(f[3], f[3], ss);
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+  const float rstd = 1.f / sqrtf(ss / 128.f + eps);
+  const f32x4 wv = load4(w, lane);
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = bf16_round(f[k] * rstd * wv[k] * silu_ref(g[k]));
+  reinterpret_cast<uint32_t*>(q)[r * 32 + lane] = fp8x4(v, inv_scale);
+}
+
+// x * sigmoid(gate) into FP8 (reference sigmoid_mul_fp8_kernel, prefill_gemm.cu:484-494): v = BF16(x / (1 +
+// e^-gate)), q = E4M3_sat(v * inv_scale); four values per thread, grid-stride.
+__global__ void __launch_bounds__(256) sigmoid_mul_fp8_kernel(const float* __restrict__ x, const float* __restrict__ gate,
+                                                              size_t quads, float inv_scale, uint8_t* __restrict__ q) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(256) + threadIdx.x; i < quads;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    const f32x4 f = load4(x, i), g = load4(gate, i);
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = bf16_round(f[k] / (1.f + __expf(-g[k])));
+    reinterpret_cast<uint32_t*>(q)[i] = fp8x4(v, inv_scale);
+  }
+}
+
+template <typename InT>
+int gated_norm_launch(const char* name, const InT* x, const InT* z, const uint16_t* w, int rows, int D, float eps,
+                      float input_scale, uint8_t* q, void* stream) {
+  const std::string nm(name);
+  if (D != 128) return fail(LQ_ERR_SHAPE, nm + ": D must be 128");
+  if (rows < 0) return fail(LQ_ERR_SHAPE, nm + ": rows must not be negative");
+  if (rows == 0) return LQ_OK;
+  if (!x || !z || !w || !q) return fail(LQ_ERR_ARG, nm + ": null pointer");
+  const uintptr_t a = sizeof(InT) * 4;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(z)) % a != 0 ||
+      (reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(q)) % 8 != 0)
+    return fail(LQ_ERR_ARG, nm + ": x and z must be " + std::to_string(a) + "-byte, w and q 8-byte aligned");
+  hipLaunchKernelGGL(gated_norm_fp8_kernel<InT>, dim3((rows + 7) / 8), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     x, z, w, static_cast<size_t>(rows), eps, 1.f / input_scale, q);
+  return check_launch(name);
+}
+
 unsigned grid_for(size_t items) {
   const size_t b = (items + 255) / 256;
   return static_cast<unsigned>(b < 8192 ? (b ? b : 1) : 8192);
@@ -221,6 +298,28 @@ int lq_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H
 int lq_rmsnorm_quant_bf16(const float* x, const uint16_t* w, uint16_t* out, int M, int H, float eps, int nvfp4,
                           float input_scale, uint8_t* q, uint8_t* sf, void* stream) {
   return rmsnorm_quant_any("rmsnorm_quant_bf16", x, w, out, true, M, H, eps, nvfp4, input_scale, q, sf, stream);
+}
+
+int lq_gated_rmsnorm_fp8(const float* x, const float* z, const uint16_t* w, int rows, int D, float eps,
+                         float input_scale, uint8_t* q, void* stream) {
+  return gated_norm_launch("gated_rmsnorm_fp8", x, z, w, rows, D, eps, input_scale, q, stream);
+}
+
+int lq_gated_rmsnorm_fp8_bf16(const uint16_t* x, const uint16_t* z, const uint16_t* w, int rows, int D, float eps,
+                              float input_scale, uint8_t* q, void* stream) {
+  return gated_norm_launch("gated_rmsnorm_fp8_bf16", x, z, w, rows, D, eps, input_scale, q, stream);
+}
+
+int lq_sigmoid_mul_fp8(const float* x, const float* gate, size_t n, float input_scale, uint8_t* q, void* stream) {
+  if (n % 4 != 0) return fail(LQ_ERR_SHAPE, "sigmoid_mul_fp8: n % 4 must be 0");
+  if (n == 0) return LQ_OK;
+  if (!x || !gate || !q) return fail(LQ_ERR_ARG, "sigmoid_mul_fp8: null pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate)) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(q) % 4 != 0)
+    return fail(LQ_ERR_ARG, "sigmoid_mul_fp8: x and gate must be 16-byte and q 4-byte aligned");
+  hipLaunchKernelGGL(sigmoid_mul_fp8_kernel, dim3(grid_for(n / 4)), dim3(256), 0, static_cast<hipStream_t>(stream), x,
+                     gate, n / 4, 1.f / input_scale, q);
+  return check_launch("sigmoid_mul_fp8");
 }
 
 }  // extern "C"

@@ -58,6 +58,9 @@ SIGNATURES = {
     "lq_quant_act_fp8": (_I, [_P, _I, _I, _F, _P, _P]),
     "lq_quant_act_fp8_bf16in": (_I, [_P, _I, _I, _F, _P, _P]),
     "lq_rmsnorm_quant_bf16": (_I, [_P, _P, _P, _I, _I, _F, _I, _F, _P, _P, _P]),
+    "lq_gated_rmsnorm_fp8": (_I, [_P, _P, _P, _I, _I, _F, _F, _P, _P]),
+    "lq_gated_rmsnorm_fp8_bf16": (_I, [_P, _P, _P, _I, _I, _F, _F, _P, _P]),
+    "lq_sigmoid_mul_fp8": (_I, [_P, _P, _SZ, _F, _P, _P]),
     "lq_prefill_gemm_fp8": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _I, _P]),
     "lq_prefill_gemm_fp8_bf16out": (_I, [_P, _I, _P, _F, _P, _I, _I, _I, _P]),
     "lq_wfile_compile": (_I, [C.c_char_p, C.c_char_p, _I, _P]),
@@ -486,6 +489,29 @@ def quant_act_fp8_bf16in(x, input_scale: float):
     M, K = x.shape
     q = torch.empty((M, K), dtype=torch.uint8, device=x.device)
     _check(lib.lq_quant_act_fp8_bf16in(_ptr(_dev(x, torch.bfloat16)), M, K, input_scale, _ptr(q), _stream()))
+    return q
+
+
+def gated_rmsnorm_fp8(x, z, w_bf16, eps: float, input_scale: float):
+    """DeltaNet output norm into FP8 (reference src/core/prefill_gemm.cu:648-660): x, z [rows][128], FP32 or both
+    BF16 (the _bf16 entry point); w BF16 [128] as int16 bits or bfloat16."""
+    rows, D = x.shape
+    if z.shape != x.shape:
+        raise ValueError("gated_rmsnorm_fp8: x and z must have the same shape")
+    q = torch.empty((rows, D), dtype=torch.uint8, device=x.device)
+    fn, dt = ((lib.lq_gated_rmsnorm_fp8_bf16, torch.bfloat16) if x.dtype == torch.bfloat16
+              else (lib.lq_gated_rmsnorm_fp8, torch.float32))
+    _check(fn(_ptr(_dev(x, dt)), _ptr(_dev(z, dt)), _ptr(_dev(w_bf16)), rows, D, eps, input_scale, _ptr(q), _stream()))
+    return q
+
+
+def sigmoid_mul_fp8(x, gate, input_scale: float):
+    """x * sigmoid(gate) into FP8 (reference src/core/prefill_gemm.cu:662-665), elementwise over x's shape."""
+    if gate.shape != x.shape:
+        raise ValueError("sigmoid_mul_fp8: x and gate must have the same shape")
+    q = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    _check(lib.lq_sigmoid_mul_fp8(_ptr(_dev(x, torch.float32)), _ptr(_dev(gate, torch.float32)), x.numel(),
+                                  input_scale, _ptr(q), _stream()))
     return q
 
 

@@ -500,6 +500,44 @@ void or_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int 
   free(v);
 }
 
+/* gated_rmsnorm_fp8 (reference gated_norm_fp8_kernel, prefill_gemm.cu:461-482, 648-653): per row of 128,
+ * lane l of 32 holds x[4l..4l+3] and forms fma(x3, x3, fma(x2, x2, fma(x1, x1, x0 * x0))); the 32 partial sums are
+ * combined by the xor butterfly (distances 16, 8, 4, 2, 1: after the step at distance o, s[l] = s[l] + s[l ^ o],
+ * the same FP32 value in both lanes); rstd = 1 / sqrtf(ss / 128 + eps); v = bf16(x * rstd * w * silu(z)) (products
+ * left to right); q = E4M3_satfinite(v * (1 / input_scale)). The BF16-input form widens x and z exactly first. */
+void or_gated_rmsnorm_fp8(const float* x, const float* z, const uint16_t* w, int rows, float eps, float input_scale,
+                          uint8_t* q) {
+  const float g = 1.f / input_scale;
+  for (int r = 0; r < rows; ++r) {
+    const float* xr = x + (size_t)r * 128;
+    const float* zr = z + (size_t)r * 128;
+    float s[32];
+    for (int l = 0; l < 32; ++l) {
+      float t = xr[4 * l] * xr[4 * l];
+      t = fmaf(xr[4 * l + 1], xr[4 * l + 1], t);
+      t = fmaf(xr[4 * l + 2], xr[4 * l + 2], t);
+      s[l] = fmaf(xr[4 * l + 3], xr[4 * l + 3], t);
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+      float t[32];
+      for (int l = 0; l < 32; ++l) t[l] = s[l] + s[l ^ o];
+      memcpy(s, t, sizeof t);
+    }
+    const float rstd = 1.f / sqrtf(s[0] / 128.f + eps);
+    for (int h = 0; h < 128; ++h) {
+      const float v = or_bf16_float(or_bf16_bits(xr[h] * rstd * or_bf16_float(w[h]) * or_silu(zr[h])));
+      q[(size_t)r * 128 + h] = or_e4m3_encode(v * g);
+    }
+  }
+}
+
+/* sigmoid_mul_fp8 (reference sigmoid_mul_fp8_kernel, prefill_gemm.cu:484-494, 662-665):
+ * q[i] = E4M3_satfinite(bf16(x[i] / (1 + expf(-gate[i]))) * (1 / input_scale)). */
+void or_sigmoid_mul_fp8(const float* x, const float* gate, size_t n, float input_scale, uint8_t* q) {
+  const float g = 1.f / input_scale;
+  for (size_t i = 0; i < n; ++i) q[i] = or_e4m3_encode(or_bf16_float(or_bf16_bits(x[i] / (1.f + expf(-gate[i])))) * g);
+}
+
 /* ------------------------------------------------------------------------------------------------ */
 /* reference GEMM                                                                                     */
 /* ------------------------------------------------------------------------------------------------ */

@@ -120,6 +120,10 @@ void or_quant_act_nvfp4(const float* x, int M, int K, float input_scale, uint8_t
 void or_silu_mul_quant_nvfp4(const float* g, const float* u, int M, int K, float input_scale, uint8_t* q, uint8_t* sf);
 void or_rmsnorm_quant(const float* x, const uint16_t* w, float* out, int M, int H, float eps, int nvfp4,
                       float input_scale, uint8_t* q, uint8_t* sf);
+/* DeltaNet gated output norm (D = 128) and attention sigmoid gate into FP8 (prefill_gemm.cu:461-494) */
+void or_gated_rmsnorm_fp8(const float* x, const float* z, const uint16_t* w, int rows, float eps, float input_scale,
+                          uint8_t* q);
+void or_sigmoid_mul_fp8(const float* x, const float* gate, size_t n, float input_scale, uint8_t* q);
 
 int or_hardware_threads(void);
 

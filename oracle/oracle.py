@@ -66,6 +66,8 @@ def _load():
         "or_quant_act_nvfp4": (None, [P, i, i, f, P, P]),
         "or_silu_mul_quant_nvfp4": (None, [P, P, i, i, f, P, P]),
         "or_rmsnorm_quant": (None, [P, P, P, i, i, f, i, f, P, P]),
+        "or_gated_rmsnorm_fp8": (None, [P, P, P, i, f, f, P]),
+        "or_sigmoid_mul_fp8": (None, [P, P, sz, f, P]),
         "or_hardware_threads": (i, []),
     }
     for name, (res, args) in sig.items():
@@ -317,6 +319,37 @@ def rmsnorm_quant(x: np.ndarray, w_bf16: np.ndarray, eps: float, nvfp4: bool, in
     lib.or_rmsnorm_quant(_p(x), _p(np.ascontiguousarray(w_bf16, np.uint16)), _p(out), M, H, eps, int(nvfp4),
                          input_scale, _p(q), _p(sf) if sf is not None else None)
     return out, q, sf
+
+
+def gated_rmsnorm_fp8(x: np.ndarray, z: np.ndarray, w_bf16: np.ndarray, eps: float, input_scale: float):
+    """DeltaNet output norm into FP8 (reference prefill_gemm.cu:461-482): x, z FP32 [rows][128] (BF16 inputs are
+    widened by the caller, exactly), w BF16 bits [128] -> q uint8 [rows][128]."""
+    x = np.ascontiguousarray(x, np.float32)
+    z = np.ascontiguousarray(z, np.float32)
+    rows, D = x.shape
+    assert D == 128 and z.shape == x.shape
+    q = np.empty((rows, D), np.uint8)
+    lib.or_gated_rmsnorm_fp8(_p(x), _p(z), _p(np.ascontiguousarray(w_bf16, np.uint16)), rows, eps, input_scale, _p(q))
+    return q
+
+
+def sigmoid_mul_fp8(x: np.ndarray, gate: np.ndarray, input_scale: float):
+    """x * sigmoid(gate) into FP8 (reference prefill_gemm.cu:484-494), elementwise."""
+    x = np.ascontiguousarray(x, np.float32)
+    gate = np.ascontiguousarray(gate, np.float32)
+    q = np.empty(x.shape, np.uint8)
+    lib.or_sigmoid_mul_fp8(_p(x), _p(gate), x.size, input_scale, _p(q))
+    return q
+
+
+def fp8_code_band(v64: np.ndarray, input_scale: float, rel: float):
+    """The FP8 codes E4M3_sat(bf16(v) * (1 / input_scale)) can take for every FP32 v within a relative `rel` of
+    the float64 value v64: (lo, hi) codes of the band's ends. BF16 rounding is monotone, so where lo == hi the code
+    is fixed, and elsewhere (a BF16 rounding boundary inside the band) it is one of the two."""
+    v64 = np.asarray(v64, np.float64)
+    a = quant_act_fp8((v64 * (1.0 - rel)).astype(np.float32), input_scale)
+    b = quant_act_fp8((v64 * (1.0 + rel)).astype(np.float32), input_scale)
+    return a, b
 
 
 def prefill_nvfp4_rows(xq, xs, rows, wv, ws, alpha: float) -> np.ndarray:

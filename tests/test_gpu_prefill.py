@@ -460,3 +460,89 @@ def test_quant_act_nvfp4_rounding_boundaries(L):
     rq, rsf = O.quant_act_nvfp4(x, 1.0)
     assert np.array_equal(sf.cpu().numpy(), rsf), "scales"
     assert np.array_equal(q.cpu().numpy(), rq), "codes"
+
+
+def _band_parity(got, ref, v64, input_scale, rel=4e-6):
+    """FP8 codes from an FP32 formula with one exp: equal to the oracle's wherever the float64 value's band of
+    `rel` fixes the code; elsewhere (a BF16 rounding boundary inside the band, where the device exp and libm expf
+    may land on either side) one of the band's two codes. Returns the fraction left to the band."""
+    lo, hi = O.fp8_code_band(v64, input_scale, rel)
+    fixed = lo == hi
+    assert np.array_equal(got[fixed], ref[fixed]), f"{int(np.sum(got[fixed] != ref[fixed]))} fixed codes differ"
+    assert np.all((got[~fixed] == lo[~fixed]) | (got[~fixed] == hi[~fixed]))
+    return float(np.mean(~fixed))
+
+
+def _gated_v64(x, z, w, eps):
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    rstd = 1.0 / np.sqrt((x64 ** 2).sum(axis=1, keepdims=True) / 128 + eps)
+    return x64 * rstd * O.bf16_to_f32(w).astype(np.float64) * (z64 / (1 + np.exp(-z64)))
+
+
+@pytest.mark.parametrize("rows", [1, 13, 4096])
+def test_gated_rmsnorm_fp8(L, rows):
+    """gated_rmsnorm_fp8 (reference prefill_gemm.cu:461-482, 648-653) against the oracle: the sum of squares,
+    rstd and the products are the same FP32 operations in the same order, so the codes are bit-exact except where
+    silu's exp may move a value across a BF16 rounding boundary (then one of the two neighbouring codes)."""
+    x = O.normal_f32(61 + rows, 1.5, (rows, 128))
+    z = O.normal_f32(62 + rows, 2.0, (rows, 128))
+    w = O.normal_bf16(63, 0.6, (128,))
+    eps, sc = 1e-6, 0.02
+    q = L.gated_rmsnorm_fp8(to_dev(x), to_dev(z), to_dev(w.view(np.int16)), eps, sc).cpu().numpy()
+    ref = O.gated_rmsnorm_fp8(x, z, w, eps, sc)
+    assert _band_parity(q, ref, _gated_v64(x, z, w, eps), sc) < 0.01
+
+
+def test_gated_rmsnorm_fp8_bf16_inputs(L):
+    """gated_rmsnorm_fp8_bf16 (reference prefill_gemm.cu:655-660): BF16 x and z give the bytes the FP32 entry point
+    gives for their exact FP32 widening, and match the oracle on that widening."""
+    rows = 300
+    xb = O.normal_bf16(71, 1.5, (rows, 128))
+    zb = O.normal_bf16(72, 2.0, (rows, 128))
+    w = O.normal_bf16(73, 0.6, (128,))
+    wd = to_dev(w.view(np.int16))
+    qb = L.gated_rmsnorm_fp8(bf16_dev(xb), bf16_dev(zb), wd, 1e-6, 0.03).cpu().numpy()
+    x, z = O.bf16_to_f32(xb), O.bf16_to_f32(zb)
+    qf = L.gated_rmsnorm_fp8(to_dev(x), to_dev(z), wd, 1e-6, 0.03).cpu().numpy()
+    assert np.array_equal(qb, qf)
+    assert _band_parity(qb, O.gated_rmsnorm_fp8(x, z, w, 1e-6, 0.03), _gated_v64(x, z, w, 1e-6), 0.03) < 0.01
+
+
+def test_gated_rmsnorm_fp8_edges(L):
+    """Known answers on the device (x = 1, w = 1, z = 20: every code E4M3(20); z = 0: zero codes; a huge w
+    saturates to 0x7E), rows = 0 does nothing, and D != 128 fails as the reference does."""
+    one = torch.ones((8, 128), dtype=torch.float32, device=DEV)
+    w1 = torch.full((128,), 0x3F80, dtype=torch.int16, device=DEV)
+    q = L.gated_rmsnorm_fp8(one, torch.full_like(one, 20.0), w1, 0.0, 1.0).cpu().numpy()
+    assert np.all(q == torch.tensor([20.0]).to(torch.float8_e4m3fn).view(torch.uint8).item())
+    assert np.all(L.gated_rmsnorm_fp8(one, torch.zeros_like(one), w1, 0.0, 1.0).cpu().numpy() & 0x7F == 0)
+    wbig = torch.full((128,), 0x4780, dtype=torch.int16, device=DEV)
+    assert np.all(L.gated_rmsnorm_fp8(one, torch.full_like(one, 20.0), wbig, 0.0, 1.0).cpu().numpy() == 0x7E)
+    assert L.gated_rmsnorm_fp8(one[:0], one[:0], w1, 1e-6, 1.0).shape == (0, 128)
+    half = torch.ones((4, 64), dtype=torch.float32, device=DEV)
+    with pytest.raises(L.LingGemmError, match="D must be 128"):
+        L.gated_rmsnorm_fp8(half, half, w1, 1e-6, 1.0)
+
+
+@pytest.mark.parametrize("shape", [(1, 4), (7, 4096), (4096, 4096)])
+def test_sigmoid_mul_fp8(L, shape):
+    """sigmoid_mul_fp8 (reference prefill_gemm.cu:484-494, 662-665) against the oracle, bit-exact outside the
+    band where the device exp and libm expf may round x / (1 + e^-g) to different BF16 neighbours."""
+    x = O.normal_f32(81 + shape[0], 3.0, shape)
+    g = O.normal_f32(82 + shape[0], 4.0, shape)
+    q = L.sigmoid_mul_fp8(to_dev(x), to_dev(g), 0.05).cpu().numpy()
+    ref = O.sigmoid_mul_fp8(x, g, 0.05)
+    v64 = x.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
+    assert _band_parity(q, ref, v64, 0.05) < 0.01
+
+
+def test_sigmoid_mul_fp8_edges(L):
+    """gate = 0 halves x, a large gate keeps it, a very negative one gives zero codes; n % 4 != 0 is refused."""
+    xs = np.array([[1.0, -3.0, 448.0, 0.5, 900.0, -0.001, 7.0, 2.5]], np.float32)
+    got = lambda gv: L.sigmoid_mul_fp8(to_dev(xs), to_dev(np.full_like(xs, gv)), 1.0).cpu().numpy()
+    assert np.array_equal(got(0.0), O.quant_act_fp8(xs / 2, 1.0))
+    assert np.array_equal(got(40.0), O.quant_act_fp8(xs, 1.0))
+    assert np.all(got(-200.0) & 0x7F == 0)
+    odd = torch.ones(6, dtype=torch.float32, device=DEV)
+    with pytest.raises(L.LingGemmError, match="n % 4"):
+        L.sigmoid_mul_fp8(odd, odd, 1.0)

@@ -480,3 +480,61 @@ def test_silu_mul_quant_nvfp4_pinned():
     q2, s2 = O.silu_mul_quant_nvfp4(neg, np.ones((1, 16), np.float32), 1.0)
     t = O.bf16_to_f32(O.f32_to_bf16(np.array([-30.0 / (1.0 + np.exp(30.0))], np.float32)))[0]
     assert s2[0, 0] == torch.tensor([abs(t) / 6.0]).to(torch.float8_e4m3fn).view(torch.uint8).item()
+
+
+def _fp8_band_check(got, v64, input_scale, rel=4e-6):
+    """got codes vs the float64 value: exact where the band fixes the code, one of the band's two codes elsewhere."""
+    lo, hi = O.fp8_code_band(v64, input_scale, rel)
+    fixed = lo == hi
+    assert np.array_equal(got[fixed], lo[fixed])
+    assert np.all((got[~fixed] == lo[~fixed]) | (got[~fixed] == hi[~fixed]))
+    return float(np.mean(~fixed))
+
+
+def test_gated_rmsnorm_fp8_oracle_pinned():
+    """gated_rmsnorm_fp8 (reference prefill_gemm.cu:461-482, 648-653) against the same formula in float64
+    (rstd from the exact sum of squares; the oracle's FP32 butterfly sum and libm expf stay within a few FP32 ulps,
+    so codes agree exactly wherever that band does not straddle a BF16 rounding boundary), and known answers
+    that a dropped / 128, a missing silu, w read as Gemma's 1 + w, or rows mixed up would break."""
+    rows = 96
+    x = O.normal_f32(41, 1.5, (rows, 128))
+    z = O.normal_f32(42, 2.0, (rows, 128))
+    w = O.normal_bf16(43, 0.6, (128,))
+    eps, sc = 1e-6, 0.02
+    q = O.gated_rmsnorm_fp8(x, z, w, eps, sc)
+    x64, z64 = x.astype(np.float64), z.astype(np.float64)
+    rstd = 1.0 / np.sqrt((x64 ** 2).sum(axis=1, keepdims=True) / 128 + eps)
+    v64 = x64 * rstd * O.bf16_to_f32(w).astype(np.float64) * (z64 / (1 + np.exp(-z64)))
+    assert _fp8_band_check(q, v64, sc) < 0.01
+    # x = 1, eps = 0: rstd = 1 exactly; w = 1, z = 20: silu(20) = 20 in FP32, so v = 20 and q = E4M3(20 / s)
+    one = np.ones((1, 128), np.float32)
+    q1 = O.gated_rmsnorm_fp8(one, np.full((1, 128), 20.0, np.float32), np.full(128, 0x3F80, np.uint16), 0.0, 1.0)
+    assert np.all(q1 == torch.tensor([20.0]).to(torch.float8_e4m3fn).view(torch.uint8).item())
+    # x = 2 everywhere: rstd = 1/2, so x * rstd = 1 again (the mean of squares, not the sum)
+    q2 = O.gated_rmsnorm_fp8(2 * one, np.full((1, 128), 20.0, np.float32), np.full(128, 0x3F80, np.uint16), 0.0, 1.0)
+    assert np.array_equal(q1, q2)
+    # z = 0 gives zero codes; w = -1 flips every sign bit
+    assert np.all(O.gated_rmsnorm_fp8(x[:2], np.zeros((2, 128), np.float32), w, eps, sc) & 0x7F == 0)
+    qn = O.gated_rmsnorm_fp8(x, z, w ^ 0x8000, eps, sc)
+    nz = (q & 0x7F) != 0
+    assert np.array_equal(qn[nz], q[nz] ^ 0x80)
+    # scaling a row by a power of two leaves its codes (eps = 0): each row is normalized on its own
+    s = (2.0 ** (np.arange(rows) % 7 - 3)).astype(np.float32).reshape(rows, 1)
+    assert np.array_equal(O.gated_rmsnorm_fp8(x * s, z, w, 0.0, sc), O.gated_rmsnorm_fp8(x, z, w, 0.0, sc))
+    # saturation: huge w pushes v * (1 / s) past 448 to the largest finite code
+    qs = O.gated_rmsnorm_fp8(one, np.full((1, 128), 20.0, np.float32), np.full(128, 0x4780, np.uint16), 0.0, 1.0)
+    assert np.all(qs == 0x7E)
+
+
+def test_sigmoid_mul_fp8_oracle_pinned():
+    """sigmoid_mul_fp8 (reference prefill_gemm.cu:484-494, 662-665) against float64 x * sigmoid(gate), and known
+    answers: gate = 0 halves x exactly, a large gate keeps x, a very negative gate gives zero."""
+    x = O.normal_f32(51, 3.0, (64, 256))
+    gt = O.normal_f32(52, 4.0, (64, 256))
+    q = O.sigmoid_mul_fp8(x, gt, 0.05)
+    v64 = x.astype(np.float64) / (1 + np.exp(-gt.astype(np.float64)))
+    assert _fp8_band_check(q, v64, 0.05) < 0.01
+    xs = np.array([[1.0, -3.0, 448.0, 0.5]], np.float32)
+    assert np.array_equal(O.sigmoid_mul_fp8(xs, np.zeros_like(xs), 1.0), O.quant_act_fp8(xs / 2, 1.0))
+    assert np.array_equal(O.sigmoid_mul_fp8(xs, np.full_like(xs, 40.0), 1.0), O.quant_act_fp8(xs, 1.0))
+    assert np.all(O.sigmoid_mul_fp8(xs, np.full_like(xs, -200.0), 1.0) & 0x7F == 0)
