@@ -66,6 +66,21 @@ class Timer:
         return sum(a.elapsed_time(b) for a, b in self.ev[:self.i]) / max(1, self.i)
 
 
+PREFILL_WARM_S = 2.0
+
+
+def warm_until(torch, fn, seconds=None):
+    """Runs fn in batches of 10 launches until `seconds` (PREFILL_WARM_S) of wall time have passed, then syncs."""
+    seconds = PREFILL_WARM_S if seconds is None else seconds
+    t0 = time.time()
+    while True:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        if time.time() - t0 >= seconds:
+            return
+
+
 _WCACHE = {}
 
 
@@ -332,10 +347,10 @@ def bench_prefill(torch, L, O, args, dev):
         a, xs = L.quant_act_fp8_g128(xb)
         del xb
         y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-        steps = max(5, args.steps // 10)
-        for _ in range(3):
-            L.prefill_fp8_block(a, xs, w, ws, N, y=y)
-        torch.cuda.synchronize()
+        steps = max(10, args.steps // 2)
+        # steady state: the part raises its clock over about a second of sustained MFMA load, so a few launches
+        # from idle read 15-20 % slow; warm up on the same GEMM for PREFILL_WARM_S seconds first
+        warm_until(torch, lambda: L.prefill_fp8_block(a, xs, w, ws, N, y=y))
         tm = Timer(torch, steps)
         for _ in range(steps):
             tm.start()
@@ -358,16 +373,14 @@ def bench_prefill(torch, L, O, args, dev):
             a = torch.randn(M, K, device=dev).to(torch.float8_e4m3fn)
             b = torch.randn(N, K, device=dev).to(torch.float8_e4m3fn)
             one = torch.tensor(1.0, device=dev)
-            for _ in range(3):
-                torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
-            torch.cuda.synchronize()
+            warm_until(torch, lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
             t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             t0.record()
-            for _ in range(10):
+            for _ in range(20):
                 torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
             t1.record()
             torch.cuda.synchronize()
-            ms = t0.elapsed_time(t1) / 10
+            ms = t0.elapsed_time(t1) / 20
             ref[name] = {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
             del a, b
         res["hipblaslt_fp8_per_tensor"] = ref
@@ -394,13 +407,11 @@ def bench_prefill_nvfp4(torch, L, args, dev):
 
     # activations x ~ N(0, 1) quantized to NVFP4 by the library's device quantizer
     xq, xs = L.quant_act_nvfp4(torch.randn((M, H), device=dev, generator=g), 1.0)
-    steps = max(5, args.steps // 20)
+    steps = max(10, args.steps // 2)
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     def timed(fn):
-        for _ in range(2):
-            fn()
-        torch.cuda.synchronize()
+        warm_until(torch, fn)  # steady-state clock, as for the FP8 prefill
         t0.record()
         for _ in range(steps):
             fn()
