@@ -535,6 +535,19 @@ def bench_producers(torch, L, dev):
     byt = 8 * nf + nf // 2 + nf // 16
     out["silu_mul_quant_nvfp4"] = line("silu", byt, timed(lambda i: L.silu_mul_quant_nvfp4(gu[i][0], gu[i][1], 0.01), c))
     del gu
+    # the DeltaNet gated output norm into FP8 (48 value heads of 128 per token) and the attention output's sigmoid
+    # gate into FP8 (24 heads of 256 per token): two FP32 inputs each
+    rows, qs = M * 48, M * 24 * 256
+    c = 2
+    xz = [(torch.randn(rows, 128, device=dev, generator=g), torch.randn(rows, 128, device=dev, generator=g))
+          for _ in range(c)]
+    wn = (torch.randn(128, device=dev, generator=g) * 0.5).to(torch.bfloat16).view(torch.int16)
+    out["gated_rmsnorm_fp8"] = line("gnorm", 9 * rows * 128 + 256, timed(
+        lambda i: L.gated_rmsnorm_fp8(xz[i][0], xz[i][1], wn, 1e-6, 0.02), c))
+    del xz
+    xg = [(torch.randn(qs, device=dev, generator=g), torch.randn(qs, device=dev, generator=g)) for _ in range(c)]
+    out["sigmoid_mul_fp8"] = line("sigm", 9 * qs, timed(lambda i: L.sigmoid_mul_fp8(xg[i][0], xg[i][1], 0.02), c))
+    del xg
     torch.cuda.empty_cache()
     # sparse-head gather: 2048 of 151936 rows of an NVFP4 [151936][5120] head, M = 17 (a verify step's rows)
     V, K, Mg, cap = 151936, 5120, 17, 2048
