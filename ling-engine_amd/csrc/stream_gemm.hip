@@ -1122,14 +1122,16 @@ int stream_args(const char* name, int fmt, bool f16, bool pair, bool outf32, con
 }
 
 // Finish workgroups when a finisher's reads would be long: a tile group spans three workgroups or more (so all
-// are split) and its partials hold (P / TG + 1) x T x G >= 48 vectors per thread. They start only as streaming
+// are split) and its partials hold (P / TG + 1) x T x G >= 24 vectors per thread. They start only as streaming
 // workgroups leave their CUs (a streaming workgroup's registers fill its CU) and see the count a memory round
-// trip later, about 2 us after the last arrival, which pays off only when one finisher's reads take longer
-// (measured: down 5120 x 17408 at M = 68 gains 13 %, the NVFP4 25600-wide fc at M = 16 2 %; the same down at
-// M = 17 or 1, or K = 6144 at M = 68, lose). The results are the same either way.
+// trip later, about 2 us after the last arrival, which pays off only when one finisher's reads take longer.
+// Measured (graph-timed, FP8 with residual): down 5120 x 17408 gains 4 % at M = 17 and 3 % at M = 33 (28
+// vectors), 13 % at M = 68; the NVFP4 25600-wide fc at M = 16 2 %. A threshold of 16 also takes K = 6144 at
+// M = 68 (20 vectors, 12 % slower) and 1024-wide matrices at M = 1 (8 % slower). The results are the same either
+// way.
 bool finish_wgs(const StreamArgs& a) {
   const int G = cdiv(a.M, 16);
-  return a.P >= 3 * a.TG && (a.P / a.TG + 1) * a.T * G >= 48;
+  return a.P >= 3 * a.TG && (a.P / a.TG + 1) * a.T * G >= 24;
 }
 
 // Arrival counters one 128-byte line apart (a stride of 32 ints) when the counter memory holds them that way, else
