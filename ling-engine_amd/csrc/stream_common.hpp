@@ -312,30 +312,33 @@ __device__ __forceinline__ int unit_start(int p, int P, int U) { return p * U / 
 struct SegSplit {
   int tgb, wgb, P, U;
 };
-template <bool PAIR>
+// ONESEG: the launch is one segment (a SiLU*mul pair, or a single matrix): segment 0, tile groups [0, TG), workgroups
+// [0, P); no argument array is then indexed by a run-time segment (such an index makes the compiler chain dependent
+// argument reads at kernel entry).
+template <bool ONESEG>
 __device__ __forceinline__ SegSplit seg_split(const StreamArgs& a, int i) {
   SegSplit s;
-  s.tgb = PAIR ? 0 : pick(a.tg0, i);
-  const int tge = PAIR ? a.TG : pick(a.tg0, i + 1);
+  s.tgb = ONESEG ? 0 : pick(a.tg0, i);
+  const int tge = ONESEG ? a.TG : pick(a.tg0, i + 1);
   s.wgb = pick(a.wg0, i);
   s.P = pick(a.wg0, i + 1) - s.wgb;
   s.U = (tge - s.tgb) * a.C;
   return s;
 }
 // The segment holding workgroup b (raw or logical: the permutation stays inside a segment), or tile group tg.
-template <bool PAIR>
+template <bool ONESEG>
 __device__ __forceinline__ int seg_of_wg(const StreamArgs& a, int b) {
   int i = 0;
-  if constexpr (!PAIR) {
+  if constexpr (!ONESEG) {
 #pragma unroll
     for (int k = 1; k < kMaxMats; ++k) i += (k < a.count && b >= a.wg0[k]) ? 1 : 0;
   }
   return i;
 }
-template <bool PAIR>
+template <bool ONESEG>
 __device__ __forceinline__ int seg_of_tg(const StreamArgs& a, int tg) {
   int i = 0;
-  if constexpr (!PAIR) {
+  if constexpr (!ONESEG) {
 #pragma unroll
     for (int k = 1; k < kMaxMats; ++k) i += (k < a.count && tg >= a.tg0[k]) ? 1 : 0;
   }
@@ -351,12 +354,12 @@ struct SegTiles {
   int toff[T], coff[T];
 };
 
-template <int WF, int T, bool PAIR>
+template <int WF, int T, bool PAIR, bool ONE = false>
 __device__ __forceinline__ void seg_tiles(const StreamArgs& a, int tg, int wave, SegTiles<WF, T, PAIR>& s) {
   // the matrix of tile group tg: the last mi < count with tg0[mi] <= tg (tg0 is increasing), counted without a
   // loop whose argument reads would wait on each other
   int mi = 0;
-  if constexpr (!PAIR) {
+  if constexpr (!PAIR && !ONE) {
 #pragma unroll
     for (int k = 1; k < kMaxMats; ++k) mi += (k < a.count && tg >= a.tg0[k]) ? 1 : 0;
   }
@@ -392,9 +395,9 @@ struct SplitInfo {
   int pf, pl;
   bool pf_first;
 };
-template <bool PAIR>
+template <bool ONESEG>
 __device__ __forceinline__ SplitInfo split_info(const StreamArgs& a, int tg) {
-  const SegSplit g = seg_split<PAIR>(a, seg_of_tg<PAIR>(a, tg));
+  const SegSplit g = seg_split<ONESEG>(a, seg_of_tg<ONESEG>(a, tg));
   const int u = (tg - g.tgb) * a.C;
   SplitInfo s;
   s.pf = g.wgb + wg_of_unit(u, g.P, g.U);
@@ -495,7 +498,7 @@ __device__ __forceinline__ void publish_partial(const StreamArgs& a, int p, int 
 constexpr int kFinishShares = 4;
 __device__ int g_wait_expired = 0;  // per device: a bounded in-kernel wait gave up (results not valid)
 
-template <int G, int T, bool PAIR, bool OUTF32>
+template <int G, int T, bool PAIR, bool OUTF32, bool ONE = false>
 __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
   const int tg = f / kFinishShares, share = f % kFinishShares;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -517,10 +520,10 @@ __device__ __forceinline__ void finish_share(const StreamArgs& a, int f) {
 #endif
   const int r = lane & 15, t = lane >> 4;
   if (tg >= a.TG) return;
-  const SplitInfo si = split_info<PAIR>(a, tg);
+  const SplitInfo si = split_info<PAIR || ONE>(a, tg);
   if (si.pf == si.pl) return;  // streamed whole by one workgroup, which finished it
   const int n = si.pl - si.pf + 1;
-  const int mi = seg_of_tg<PAIR>(a, tg);
+  const int mi = seg_of_tg<PAIR || ONE>(a, tg);
   const int wtile0 = (tg - pick(a.tg0, mi)) * (group_rows(T, PAIR) / 16) + share * (PAIR ? T / 2 : T);
   // units of the share: (tile, group) vectors, a SiLU*mul pair's gate and up vector together; wave w takes
   // units w, w + 4, ...
@@ -714,10 +717,10 @@ struct NoWait {
 
 // Logical workgroup id: blockIdx.x % 8 is the XCD the hardware places it on; consecutive logical ids share an
 // XCD, so a tile group's partials are exchanged within one L2.
-template <bool PAIR>
+template <bool ONESEG>
 __device__ __forceinline__ int logical_wg(const StreamArgs& a) {
   const int b = blockIdx.x;
-  const SegSplit g = seg_split<PAIR>(a, seg_of_wg<PAIR>(a, b));
+  const SegSplit g = seg_split<ONESEG>(a, seg_of_wg<ONESEG>(a, b));
   const int bl = b - g.wgb;
   int p = bl;
   if ((g.P & 7) == 0 && (g.wgb & 7) == 0) p = (bl & 7) * (g.P >> 3) + (bl >> 3);

@@ -47,7 +47,8 @@ namespace lq {
 namespace {
 // NPRE (with kXCoh only): the range's first NPRE chunks run ahead (see the prologue), with their activation images and
 // wave 0's weights in xpre.
-template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, int MODE, int NPRE = 0, class Ready>
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, int MODE, bool ONE = false, int NPRE = 0,
+          class Ready>
 __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>& sm, Ready&& ready,
                                             uint8_t* xpre = nullptr) {
   constexpr int T = TW;
@@ -90,7 +91,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   }
 
   // this workgroup's units, in the global (tile group, chunk) numbering
-  const SegSplit seg = seg_split<PAIR>(a, seg_of_wg<PAIR>(a, p));
+  const SegSplit seg = seg_split<PAIR || ONE>(a, seg_of_wg<PAIR || ONE>(a, p));
   const int u0 = seg.tgb * a.C + unit_start(p - seg.wgb, seg.P, seg.U);
   const int u1 = seg.tgb * a.C + unit_start(p - seg.wgb + 1, seg.P, seg.U);
   const int n_it = u1 - u0;  // chunks this workgroup streams
@@ -120,7 +121,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   // boundaries: the load cursor (ltg, lc) runs PF - 1 chunks ahead of the compute cursor (ctg, cc).
   int ltg = tg_first, lc = cfirst, lleft = n_it;
   SegTiles<WF, T, PAIR> L;
-  seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
+  seg_tiles<WF, T, PAIR, ONE>(a, ltg, wave, L);
   LQ_TS(11);
   int ctg = tg_first, cc = cfirst;
   int cmi = L.mi, cwtile0 = L.wtile0;
@@ -142,7 +143,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
       if (++lc == a.C) {
         lc = 0;
         ++ltg;
-        if (lleft > 0) seg_tiles<WF, T, PAIR>(a, ltg, wave, L);
+        if (lleft > 0) seg_tiles<WF, T, PAIR, ONE>(a, ltg, wave, L);
       }
     }
   };
@@ -239,7 +240,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
       ++ctg;
       cc = 0;
       SegTiles<WF, T, PAIR> s;
-      seg_tiles<WF, T, PAIR>(a, ctg, wave, s);
+      seg_tiles<WF, T, PAIR, ONE>(a, ctg, wave, s);
       cmi = s.mi;
       cwtile0 = s.wtile0;
     }
@@ -251,8 +252,8 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
 
   // The epilogue inputs of the range's first and last tile groups, read ahead of the weight stream.
   SegTiles<WF, T, PAIR> sF, sL;
-  seg_tiles<WF, T, PAIR>(a, tg_first, wave, sF);
-  seg_tiles<WF, T, PAIR>(a, tg_last, wave, sL);
+  seg_tiles<WF, T, PAIR, ONE>(a, tg_first, wave, sF);
+  seg_tiles<WF, T, PAIR, ONE>(a, tg_last, wave, sL);
   EpiIn<G, T> eF, eL;
   epi_load<G, PAIR, OUTF32, T>(a, sF.mi, sF.wtile0, eF, r, t);
   LQ_TS(12);
@@ -481,7 +482,7 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
     flush_trace(p);
     return;
   }
-  const SplitInfo si[2] = {split_info<PAIR>(a, tg_first), split_info<PAIR>(a, tg_last)};
+  const SplitInfo si[2] = {split_info<PAIR || ONE>(a, tg_first), split_info<PAIR || ONE>(a, tg_last)};
   // (selects rather than indexing si by thread: a thread-indexed local array would be placed in LDS)
   if (threadIdx.x < 2) {
     const bool h = threadIdx.x != 0;
@@ -524,14 +525,14 @@ __device__ __forceinline__ void stream_body(const StreamArgs& a, int p, Smem<G>&
   flush_trace(p);
 }
 
-template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT = false>
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT = false, bool ONE = false>
 __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   __shared__ __attribute__((aligned(16))) Smem<G> sm;
   if (static_cast<int>(blockIdx.x) >= a.P) {
-    finish_share<G, TW, PAIR, OUTF32>(a, static_cast<int>(blockIdx.x) - a.P);
+    finish_share<G, TW, PAIR, OUTF32, ONE>(a, static_cast<int>(blockIdx.x) - a.P);
     return;
   }
-  stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0>(a, logical_wg<PAIR>(a), sm, NoWait{});
+  stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0, ONE>(a, logical_wg<PAIR || ONE>(a), sm, NoWait{});
 }
 
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
@@ -587,7 +588,7 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
   // Phase B runs on its own split's b.P <= P workgroups (the first b.P blocks, mapped as a launch of b alone would
   // map them); the rest only count themselves out below.
   if (static_cast<int>(blockIdx.x) < b.P)
-    stream_body<G, kFp8, 2, false, false, false, kXCoh, NPRE>(b, logical_wg<false>(b), sm, ready, xpre);
+    stream_body<G, kFp8, 2, false, false, false, kXCoh, true, NPRE>(b, logical_wg<true>(b), sm, ready, xpre);
   __syncthreads();
   if (threadIdx.x == 0 &&
       __hip_atomic_fetch_add(sync + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == P - 1) {
@@ -998,8 +999,21 @@ int choose_wgs(long long U) {
 
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g(const StreamArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), dim3(a.P + a.NR * a.TG), dim3(kThreads), 0,
-                     s, a);
+  // One matrix (or one pair): its segment is 0 at compile time, so no argument read waits on a computed segment
+  // index (about 1 us less before the first weight load). Only the FP16-in, FP32-out entry points take several
+  // matrices per launch (stream_gemm_multi); only they also instantiate the general form.
+  const dim3 grid(a.P + a.NR * a.TG);
+  if constexpr (PAIR) {
+    hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), grid, dim3(kThreads), 0, s, a);
+  } else if constexpr (F16 && OUTF32 && !CVT) {
+    if (a.count == 1)
+      hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT, true>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (a.count != 1) return fail(LQ_ERR_ARG, "stream_gemm: one matrix per launch with BF16 activations or output");
+    hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT, true>), grid, dim3(kThreads), 0, s, a);
+  }
   return check_launch("stream_gemm");
 }
 
