@@ -1048,11 +1048,11 @@ unsigned long long* g_trace = nullptr;  // device buffer of P x 8 stamps for the
 size_t slot_floats(int T, int M) { return static_cast<size_t>(T) * cdiv(M, 16) * 4 * kThreads; }
 
 // Tiles per wave, tile groups and workgroups of one matrix (or one SiLU*mul pair) launched alone. One FP8 tile per
-// wave when a workgroup's range would be short (under 7 chunks at two tiles) and a tile group would span more than
-// 4 workgroups: there the finish dominates, and one tile per wave halves its fan-in and partial size. (Under 10
-// chunks measured 3 % slower on 5120 x 6144 at M = 17 and 49, and the M = 68 decode-step pass 2.5 % slower: one tile
-// per wave stages a chunk's activations for half the weight bytes.) Depends on the matrix's N, K and the device
-// only, never on M (row invariance).
+// wave when a workgroup's range would be short (under 10 chunks at two tiles) and a tile group would span six
+// workgroups or more: there the finish dominates, and one tile per wave halves its fan-in and partial size. A lower
+// fan-in does not pay for the activations one tile per wave stages per weight byte (twice as many): 7168 x 5120
+// (fan-in 4.6) is 2 % slower over the M = 68 decode-step pass with one tile, 5120 x 6144 (fan-in 6) 3-6 % faster at
+// M = 17..68. Depends on the matrix's N, K and the device only, never on M (row invariance).
 void matrix_split(int fmt, bool pair, int N, int C, int& T, int& tg, int& P) {
   T = tiles_per_wave(fmt, pair);
   auto go = [&]() {
@@ -1065,7 +1065,7 @@ void matrix_split(int fmt, bool pair, int N, int C, int& T, int& tg, int& P) {
     if (!pair && P >= 3 * tg && (P % tg) * 16 <= P) P -= P % tg;
   };
   go();
-  if (fmt == kFp8 && !pair && static_cast<long long>(tg) * C < 7LL * P && P > 4 * tg) {
+  if (fmt == kFp8 && !pair && static_cast<long long>(tg) * C < 10LL * P && P > 5 * tg) {
     T = 1;
     go();
   }
