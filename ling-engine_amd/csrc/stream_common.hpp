@@ -31,11 +31,12 @@ __host__ __device__ constexpr int group_rows(int T, bool pair) { return 16 * 4 *
 // stages add no bandwidth but lengthen the prologue (all of them are issued before the first chunk is computed) and
 // the registers they hold. Measured against the earlier register-budget depths (12/10/8/6 at one tile, 8/6/4 at two,
 // 6/4/3/2 at four): verify step at M = 17 56.2 -> 53.7 us, the NVFP4 fc 8-12 % faster, FP8 launches under 10 us
-// 15-20 % faster, no shape slower.
+// 15-20 % faster, no shape slower; two stages at two tiles from G = 3 (the operand prefetch of G <= 2 needs three)
+// another 1-3 % at M = 33..68.
 template <int T>
 __host__ __device__ constexpr int pf_stages(int G) {
   return T == 1   ? (G <= 1 ? 5 : 4)
-         : T == 2 ? 3
+         : T == 2 ? (G <= 2 ? 3 : 2)
                   : (G <= 3 ? 3 : 2);
 }
 
