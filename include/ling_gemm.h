@@ -154,7 +154,8 @@ int lq_stream_fp8_pc_residual(const uint16_t* x, int M, const uint8_t* w, const 
  * the two calls' results. The launch keeps every workgroup resident (one per CU) and hands h from the first
  * phase to the second inside the kernel: only one such launch may run on a device at a time. Replaces the
  * reference's persistent FFN kernel (reference src/core/stream_gemm.cu:841-1072, ffn_step) for the FP8 rows path.
- * Experimental: it runs level with the two calls on MI355X, not faster; prefer them unless one launch is required. */
+ * Experimental: it runs slower than the two calls on MI355X (about 2 us at M = 17); prefer them unless one launch
+ * is required. */
 int lq_stream_fp8_pc_ffn(const uint16_t* x, int M, const uint8_t* w_gate, const float* s_gate, const uint8_t* w_up,
                          const float* s_up, const uint8_t* w_down, const float* s_down, const uint16_t* resid,
                          uint16_t* h, uint16_t* y, int I, int H, void* stream);
