@@ -367,22 +367,34 @@ def bench_prefill(torch, L, O, args, dev):
     res["total"] = {"flop": total_flop, "ms": total_ms, "tflops": total_flop / (total_ms * 1e-3) / 1e12,
                     "frac_mfma": total_flop / (total_ms * 1e-3) / 1e12 / FP8_DENSE_TFLOPS}
     if args.vendor_reference:
-        # a comparison point only (not this library's path): the vendor GEMM with one scale per tensor
+        # a comparison point only (not this library's path): the vendor GEMM with one scale per tensor, and this
+        # library's two forms on the same operands
         ref = {}
         for name, N, K in (("gate_up", 2 * F, H), ("down", H, F)):
             a = torch.randn(M, K, device=dev).to(torch.float8_e4m3fn)
             b = torch.randn(N, K, device=dev).to(torch.float8_e4m3fn)
             one = torch.tensor(1.0, device=dev)
-            warm_until(torch, lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16))
-            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0.record()
-            for _ in range(20):
-                torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one, out_dtype=torch.bfloat16)
-            t1.record()
-            torch.cuda.synchronize()
-            ms = t0.elapsed_time(t1) / 20
-            ref[name] = {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
-            del a, b
+            # the same operands through this library: the per-tensor form and the block-scaled one (unit scales)
+            w = L.retile_fp8(b.view(torch.uint8).contiguous())
+            xs1 = torch.ones((M, K // 128), device=dev)
+            ws1 = torch.ones((N // 128, K // 128), device=dev)
+            yb = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            runs = {"hipblaslt_per_tensor": lambda: torch._scaled_mm(a, b.t(), scale_a=one, scale_b=one,
+                                                                     out_dtype=torch.bfloat16),
+                    "per_tensor_here": lambda: L.prefill_gemm_fp8_bf16out(a.view(torch.uint8), w, 1.0, N, y=yb),
+                    "block_scaled_here": lambda: L.prefill_fp8_block(a.view(torch.uint8), xs1, w, ws1, N, y=yb)}
+            ref[name] = {}
+            for key, fn in runs.items():
+                warm_until(torch, fn)
+                t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                t0.record()
+                for _ in range(20):
+                    fn()
+                t1.record()
+                torch.cuda.synchronize()
+                ms = t0.elapsed_time(t1) / 20
+                ref[name][key] = {"ms": ms, "tflops": 2.0 * M * N * K / (ms * 1e-3) / 1e12}
+            del a, b, w, yb
         res["hipblaslt_fp8_per_tensor"] = ref
     torch.cuda.empty_cache()
     return res
