@@ -646,17 +646,21 @@ struct GatherDepth {
 // lanes of the group get values of rows past M, whose MFMA columns are never stored. The MFMA operands of every
 // stored column are the same as with four loads, so the results are too; it saves three of the wave's loads per
 // chunk.
-template <int G, bool ONE>
+// SPLIT: one token group per workgroup (blockIdx.y): a wave per 16 gathered rows and 16 tokens, so M = 17..80
+// fills 2..5 times the waves of one wave carrying every group. An MFMA output column's sum depends on that
+// column's operands only, so each element is the same either way.
+template <int G, bool ONE, bool SPLIT = false>
 __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, t = lane >> 4;
   const int cnt = min(max(*a.nrows, 0), a.cap);
   const int i0 = static_cast<int>(blockIdx.x) * 16;  // this wave's first gathered row
-  // epilogue rows of this lane: gathered i = i0 + 4t + v, token 16g + r
+  const int m0 = SPLIT ? 16 * static_cast<int>(blockIdx.y) : 0;  // this wave's first token
+  // epilogue rows of this lane: gathered i = i0 + 4t + v, token m0 + 16g + r
   auto store = [&](const float (&val)[G][4]) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const int m = 16 * g + r;
+      const int m = m0 + 16 * g + r;
       if (m >= a.M) continue;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -701,7 +705,7 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
   unsigned xoff[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int m = 16 * g + r;
+    const int m = m0 + 16 * g + r;
     xoff[g] = m < a.M ? static_cast<unsigned>(m * a.K * 2 + t * 64) : 0x80000000u;
   }
   // ONE: lane r < 4 of the last group loads piece r of row M - 1 (16 * (G - 1))
@@ -797,20 +801,12 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
   float val[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int m = 16 * g + r;
+    const int m = m0 + 16 * g + r;
     const float xi = m < a.M ? a.xinv[m] : 1.f;
 #pragma unroll
     for (int v = 0; v < 4; ++v) val[g][v] = (tot[g][v] * a.scale2) * xi;
   }
   store(val);
-}
-
-template <int G>
-void launch_gather(int M, dim3 grid, dim3 blk, hipStream_t s, const GatherArgs& a) {
-  if (M % 16 == 1)
-    hipLaunchKernelGGL((gather_kernel<G, true>), grid, blk, 0, s, a);
-  else
-    hipLaunchKernelGGL((gather_kernel<G, false>), grid, blk, 0, s, a);
 }
 
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
@@ -1531,13 +1527,11 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.U = ftg * a.C;
   const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  switch (cdiv(M, 16)) {
-    case 1: launch_gather<1>(M, grid, blk, s, a); break;
-    case 2: launch_gather<2>(M, grid, blk, s, a); break;
-    case 3: launch_gather<3>(M, grid, blk, s, a); break;
-    case 4: launch_gather<4>(M, grid, blk, s, a); break;
-    default: launch_gather<5>(M, grid, blk, s, a); break;
-  }
+  // one token group per workgroup row; a single token takes the one-row form
+  if (M == 1)
+    hipLaunchKernelGGL((gather_kernel<1, true>), grid, blk, 0, s, a);
+  else
+    hipLaunchKernelGGL((gather_kernel<1, false, true>), dim3(cap / 16, cdiv(M, 16)), blk, 0, s, a);
   return check_launch("stream_gemm_gather");
 }
 
