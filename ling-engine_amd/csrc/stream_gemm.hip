@@ -44,6 +44,16 @@
 #include <utility>
 
 namespace lq {
+// FP8 launches whose kernels run faster with MFMA accumulators in VGPRs (-mllvm -amdgpu-mfma-vgpr-form, a
+// per-translation-unit switch): this file is compiled a second time with it and LQ_STREAM_VGPR_TU defined,
+// keeping only the kernels and launch_g_vgpr. Measured per kernel against the AGPR form (rocprofv3, the
+// verify, decode-step, shape and fc workloads): 0.4-9 % faster for every FP8 kernel with one or two tiles per
+// wave up to three token groups and with one tile per wave at four or five (verify gate|up 2.3 %, down 3.2 %),
+// 2-4 % slower with two tiles at five; the NVFP4 kernels do not change. The same arithmetic either way.
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
+int launch_g_vgpr(const StreamArgs& a, hipStream_t s);
+constexpr bool vgpr_form(int G, int WF, int TW) { return WF == kFp8 && (G <= 3 || TW == 1); }
+
 namespace {
 // NPRE (with kXCoh only): the range's first NPRE chunks run ahead (see the prologue), with their activation images and
 // wave 0's weights in xpre.
@@ -535,6 +545,7 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0, ONE>(a, logical_wg<PAIR || ONE>(a), sm, NoWait{});
 }
 
+#ifndef LQ_STREAM_VGPR_TU
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
 // with SiLU(gate) * up into h (a), phase B = down (+ residual) from h (b). Both phases use the same P and the
 // same split as two separate launches, so every output is bit for bit theirs. Each workgroup ends phase A
@@ -649,8 +660,11 @@ struct GatherDepth {
 // SPLIT: one token group per workgroup (blockIdx.y): a wave per 16 gathered rows and 16 tokens, so M = 17..80
 // fills 2..5 times the waves of one wave carrying every group. An MFMA output column's sum depends on that
 // column's operands only, so each element is the same either way.
+// amdgpu_waves_per_eu(2) caps the kernel at 256 registers, so its MFMAs accumulate in VGPRs (251 used, no
+// AGPRs): with the accumulator in AGPRs the compiler copies it out before every cut test, which waits for the
+// chunk's whole MFMA chain.
 template <int G, bool ONE, bool SPLIT = false>
-__global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs a) {
+__global__ void __launch_bounds__(kGatherThreads) __attribute__((amdgpu_waves_per_eu(2))) gather_kernel(const GatherArgs a) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, t = lane >> 4;
   const int cnt = min(max(*a.nrows, 0), a.cap);
@@ -688,6 +702,13 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
   const int nac = aoob ? 0 : na;
   const int slot = (nac & 15) * 4 + t;
   // the lane's output rows: their tile groups and next cuts
+  // (wg_of_unit and unit_start by div_by_rcp: the host bounds U below 2^19 and (U + 1) * (P + 1) below 2^31, and a cut
+  // inside the chunk loop then costs a few instructions, not two integer divisions on the wave's serial path)
+  const float rP = 1.f / static_cast<float>(a.P), rU = 1.f / static_cast<float>(a.U);
+  auto next_cut = [&](int u, int tg0) {  // the last chunk of the workgroup that holds unit u, relative to tg0
+    const int p = div_by_rcp((u + 1) * a.P - 1, a.U, rU);
+    return min(a.C - 1, div_by_rcp((p + 1) * a.U, a.P, rP) - 1 - tg0);
+  };
   int tgc[4], nb[4];
   bool first[4];
 #pragma unroll
@@ -696,8 +717,7 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
     int no = io < cnt ? a.rows[io] : 0;
     no = (no >= 0 && no < a.N) ? no : 0;
     tgc[v] = (no / a.TGR) * a.C;
-    const int p = wg_of_unit(tgc[v], a.P, a.U);
-    nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+    nb[v] = next_cut(tgc[v], tgc[v]);
     first[v] = true;
   }
   // the lane's activation bytes: row 16g + r from byte 64t of each chunk (rows >= M read as zeros)
@@ -773,7 +793,6 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
 #pragma unroll
         for (int s = 0; s < 4; ++s) xb[g][s] = xr[j][g][s];
       }
-      issue(J, c + D);
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         u32x4 b[G];
@@ -781,18 +800,27 @@ __global__ void __launch_bounds__(kGatherThreads) gather_kernel(const GatherArgs
         for (int g = 0; g < G; ++g) b[g] = xb[g][s];
         mfma_step<kFp4, true, G, 1>(R, s, b, acc, tab);
       }
+      // refill slot j only after its operands are consumed: issued before the MFMAs, the new and the old values
+      // are live together, and the compiler reconciles the two register sets with copies at the loop's back
+      // edge that wait for every load in flight, draining the ring every D chunks
+      issue(J, c + D);
+      // a cut is rare (a row's tile group ends or its workgroup changes): one wave-uniform test first, so the
+      // common path never reads the accumulator (a read waits for the chunk's whole MFMA chain, and without
+      // the test the compiler hoists the reads out of the per-row branches)
+      bool cut = false;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        if (c == nb[v]) {
+      for (int v = 0; v < 4; ++v) cut |= c == nb[v];
+      if (__builtin_amdgcn_ballot_w64(cut)) {
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            tot[g][v] = first[v] ? acc[0][g][v] : tot[g][v] + acc[0][g][v];
-            acc[0][g][v] = 0.f;
-          }
-          first[v] = false;
-          if (c + 1 < a.C) {
-            const int p = wg_of_unit(tgc[v] + c + 1, a.P, a.U);
-            nb[v] = min(a.C - 1, unit_start(p + 1, a.P, a.U) - 1 - tgc[v]);
+        for (int v = 0; v < 4; ++v) {
+          if (c == nb[v]) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+              tot[g][v] = first[v] ? acc[0][g][v] : tot[g][v] + acc[0][g][v];
+              acc[0][g][v] = 0.f;
+            }
+            first[v] = false;
+            if (c + 1 < a.C) nb[v] = next_cut(tgc[v] + c + 1, tgc[v]);
           }
         }
       }
@@ -993,8 +1021,10 @@ int choose_wgs(long long U) {
   return static_cast<int>(std::max<long long>(P, 1));
 }
 
+#endif  // LQ_STREAM_VGPR_TU
+
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
-int launch_g(const StreamArgs& a, hipStream_t s) {
+int launch_g_here(const StreamArgs& a, hipStream_t s) {
   // One matrix (or one pair): its segment is 0 at compile time, so no argument read waits on a computed segment
   // index (about 1 us less before the first weight load). Only the FP16-in, FP32-out entry points take several
   // matrices per launch (stream_gemm_multi); only they also instantiate the general form.
@@ -1011,6 +1041,15 @@ int launch_g(const StreamArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((stream_kernel<G, WF, TW, F16, PAIR, OUTF32, CVT, true>), grid, dim3(kThreads), 0, s, a);
   }
   return check_launch("stream_gemm");
+}
+
+#ifndef LQ_STREAM_VGPR_TU
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
+int launch_g(const StreamArgs& a, hipStream_t s) {
+  if constexpr (vgpr_form(G, WF, TW))
+    return launch_g_vgpr<G, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+  else
+    return launch_g_here<G, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
 }
 
 template <int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
@@ -1525,6 +1564,8 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   a.TGR = group_rows(fT, false);
   a.P = fP;
   a.U = ftg * a.C;
+  if (a.U >= (1 << 19) || (static_cast<long long>(a.U) + 1) * (a.P + 1) >= (1LL << 31))
+    return fail(LQ_ERR_SHAPE, nm + ": too many units for the gather's split arithmetic");
   const dim3 grid(cap / 16), blk(kGatherThreads);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   // one token group per workgroup row; a single token takes the one-row form
@@ -1566,3 +1607,30 @@ int lq_stream_nvfp4_bf16(const uint16_t* x, int M, const uint8_t* w, const uint8
 }
 
 }  // extern "C"
+
+#else  // LQ_STREAM_VGPR_TU: the FP8 kernels vgpr_form selects, compiled with VGPR accumulators
+
+}  // namespace
+
+template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
+int launch_g_vgpr(const StreamArgs& a, hipStream_t s) {
+  return launch_g_here<G, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
+}
+
+// every launch the main translation unit routes here: single matrices (BF16 or FP16 activations, BF16 or FP32
+// output) at one or two tiles per wave, SiLU*mul pairs at two
+#define LQ_VGPR_SINGLE(G, TW)                                                                       \
+  template int launch_g_vgpr<G, kFp8, TW, false, false, false, false>(const StreamArgs&, hipStream_t); \
+  template int launch_g_vgpr<G, kFp8, TW, false, false, true, false>(const StreamArgs&, hipStream_t);  \
+  template int launch_g_vgpr<G, kFp8, TW, true, false, false, false>(const StreamArgs&, hipStream_t);  \
+  template int launch_g_vgpr<G, kFp8, TW, true, false, true, false>(const StreamArgs&, hipStream_t);
+#define LQ_VGPR_PAIR(G)                                                                            \
+  template int launch_g_vgpr<G, kFp8, 2, false, true, false, false>(const StreamArgs&, hipStream_t); \
+  template int launch_g_vgpr<G, kFp8, 2, true, true, false, false>(const StreamArgs&, hipStream_t);
+LQ_VGPR_SINGLE(1, 1) LQ_VGPR_SINGLE(2, 1) LQ_VGPR_SINGLE(3, 1) LQ_VGPR_SINGLE(4, 1) LQ_VGPR_SINGLE(5, 1)
+LQ_VGPR_SINGLE(1, 2) LQ_VGPR_SINGLE(2, 2) LQ_VGPR_SINGLE(3, 2)
+LQ_VGPR_PAIR(1) LQ_VGPR_PAIR(2) LQ_VGPR_PAIR(3)
+static_assert(vgpr_form(3, kFp8, 2) && vgpr_form(5, kFp8, 1) && !vgpr_form(4, kFp8, 2) && !vgpr_form(1, kFp4, 4),
+              "the instantiations above cover vgpr_form");
+}  // namespace lq
+#endif  // LQ_STREAM_VGPR_TU
