@@ -49,10 +49,11 @@ namespace lq {
 // keeping only the kernels and launch_g_vgpr. Measured per kernel against the AGPR form (rocprofv3, the
 // verify, decode-step, shape and fc workloads): 0.4-9 % faster for every FP8 kernel with one or two tiles per
 // wave up to three token groups and with one tile per wave at four or five (verify gate|up 2.3 %, down 3.2 %),
-// 2-4 % slower with two tiles at five; the NVFP4 kernels do not change. The same arithmetic either way.
+// the verify step at M = 49 and 64 (two tiles, four groups) 5 % faster, 2-4 % slower with two tiles at five;
+// the NVFP4 kernels do not change. The same arithmetic either way.
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g_vgpr(const StreamArgs& a, hipStream_t s);
-constexpr bool vgpr_form(int G, int WF, int TW) { return WF == kFp8 && (G <= 3 || TW == 1); }
+constexpr bool vgpr_form(int G, int WF, int TW) { return WF == kFp8 && (G <= 4 || TW == 1); }
 
 namespace {
 // NPRE (with kXCoh only): the range's first NPRE chunks run ahead (see the prologue), with their activation images and
@@ -1618,7 +1619,7 @@ int launch_g_vgpr(const StreamArgs& a, hipStream_t s) {
 }
 
 // every launch the main translation unit routes here: single matrices (BF16 or FP16 activations, BF16 or FP32
-// output) at one or two tiles per wave, SiLU*mul pairs at two
+// output) at one or two tiles per wave, SiLU*mul pairs at two (two tiles only up to four token groups)
 #define LQ_VGPR_SINGLE(G, TW)                                                                       \
   template int launch_g_vgpr<G, kFp8, TW, false, false, false, false>(const StreamArgs&, hipStream_t); \
   template int launch_g_vgpr<G, kFp8, TW, false, false, true, false>(const StreamArgs&, hipStream_t);  \
@@ -1628,9 +1629,9 @@ int launch_g_vgpr(const StreamArgs& a, hipStream_t s) {
   template int launch_g_vgpr<G, kFp8, 2, false, true, false, false>(const StreamArgs&, hipStream_t); \
   template int launch_g_vgpr<G, kFp8, 2, true, true, false, false>(const StreamArgs&, hipStream_t);
 LQ_VGPR_SINGLE(1, 1) LQ_VGPR_SINGLE(2, 1) LQ_VGPR_SINGLE(3, 1) LQ_VGPR_SINGLE(4, 1) LQ_VGPR_SINGLE(5, 1)
-LQ_VGPR_SINGLE(1, 2) LQ_VGPR_SINGLE(2, 2) LQ_VGPR_SINGLE(3, 2)
-LQ_VGPR_PAIR(1) LQ_VGPR_PAIR(2) LQ_VGPR_PAIR(3)
-static_assert(vgpr_form(3, kFp8, 2) && vgpr_form(5, kFp8, 1) && !vgpr_form(4, kFp8, 2) && !vgpr_form(1, kFp4, 4),
+LQ_VGPR_SINGLE(1, 2) LQ_VGPR_SINGLE(2, 2) LQ_VGPR_SINGLE(3, 2) LQ_VGPR_SINGLE(4, 2)
+LQ_VGPR_PAIR(1) LQ_VGPR_PAIR(2) LQ_VGPR_PAIR(3) LQ_VGPR_PAIR(4)
+static_assert(vgpr_form(4, kFp8, 2) && vgpr_form(5, kFp8, 1) && !vgpr_form(5, kFp8, 2) && !vgpr_form(1, kFp4, 4),
               "the instantiations above cover vgpr_form");
 }  // namespace lq
 #endif  // LQ_STREAM_VGPR_TU
