@@ -54,6 +54,10 @@ namespace lq {
 template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g_vgpr(const StreamArgs& a, hipStream_t s);
 constexpr bool vgpr_form(int G, int WF, int TW) { return WF == kFp8 && (G <= 4 || TW == 1); }
+// The one-launch FFN (phase A: a gate|up pair, phase B: a single matrix, two tiles per wave each) likewise up
+// to four token groups (ffn_kernel<2> 56.3 -> 55.2 us, rocprofv3).
+template <int G>
+void launch_ffn_vgpr(const StreamArgs& a, const StreamArgs& b, int* sync, hipStream_t s);
 
 namespace {
 // NPRE (with kXCoh only): the range's first NPRE chunks run ahead (see the prologue), with their activation images and
@@ -546,7 +550,6 @@ __global__ void __launch_bounds__(kThreads) stream_kernel(const StreamArgs a) {
   stream_body<G, WF, TW, F16, PAIR, OUTF32, CVT ? kCvt : 0, ONE>(a, logical_wg<PAIR || ONE>(a), sm, NoWait{});
 }
 
-#ifndef LQ_STREAM_VGPR_TU
 // The FFN step in one launch (reference persistent FFN, src/core/stream_gemm.cu:841-1072): phase A = gate|up
 // with SiLU(gate) * up into h (a), phase B = down (+ residual) from h (b). Both phases use the same P and the
 // same split as two separate launches, so every output is bit for bit theirs. Each workgroup ends phase A
@@ -610,6 +613,7 @@ __global__ void __launch_bounds__(kThreads) ffn_kernel(const StreamArgs a, const
   }
 }
 
+#ifndef LQ_STREAM_VGPR_TU
 // ---------------- gathered rows (reference stream_gemm_gather_nvfp4, src/core/stream_gemm.cu:1902-1923) -------------
 // y[m][i] = scale2 * x[m] . W[rows[i]] * xinv[m] for i < *nrows, -inf for nrows <= i < cap, with every element's
 // arithmetic that of the full NVFP4 launch over all N rows (so a selected row's logit is bit for bit the full
@@ -1296,10 +1300,10 @@ int ffn_launch(const char* name, const uint16_t* x, int M, const Mat (&gu)[2], c
   b.trace = g_trace ? g_trace + 16 * static_cast<size_t>(a.P) : nullptr;
 #endif
   switch (cdiv(M, 16)) {
-    case 1: hipLaunchKernelGGL(ffn_kernel<1>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
-    case 2: hipLaunchKernelGGL(ffn_kernel<2>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
-    case 3: hipLaunchKernelGGL(ffn_kernel<3>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
-    case 4: hipLaunchKernelGGL(ffn_kernel<4>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
+    case 1: launch_ffn_vgpr<1>(a, b, ws->sync, s); break;
+    case 2: launch_ffn_vgpr<2>(a, b, ws->sync, s); break;
+    case 3: launch_ffn_vgpr<3>(a, b, ws->sync, s); break;
+    case 4: launch_ffn_vgpr<4>(a, b, ws->sync, s); break;
     default: hipLaunchKernelGGL(ffn_kernel<5>, dim3(a.P), dim3(kThreads), 0, s, a, b, ws->sync); break;
   }
   return check_launch(name);
@@ -1617,6 +1621,15 @@ template <int G, int WF, int TW, bool F16, bool PAIR, bool OUTF32, bool CVT>
 int launch_g_vgpr(const StreamArgs& a, hipStream_t s) {
   return launch_g_here<G, WF, TW, F16, PAIR, OUTF32, CVT>(a, s);
 }
+
+template <int G>
+void launch_ffn_vgpr(const StreamArgs& a, const StreamArgs& b, int* sync, hipStream_t s) {
+  hipLaunchKernelGGL(ffn_kernel<G>, dim3(a.P), dim3(kThreads), 0, s, a, b, sync);
+}
+template void launch_ffn_vgpr<1>(const StreamArgs&, const StreamArgs&, int*, hipStream_t);
+template void launch_ffn_vgpr<2>(const StreamArgs&, const StreamArgs&, int*, hipStream_t);
+template void launch_ffn_vgpr<3>(const StreamArgs&, const StreamArgs&, int*, hipStream_t);
+template void launch_ffn_vgpr<4>(const StreamArgs&, const StreamArgs&, int*, hipStream_t);
 
 // every launch the main translation unit routes here: single matrices (BF16 or FP16 activations, BF16 or FP32
 // output) at one or two tiles per wave, SiLU*mul pairs at two (two tiles only up to four token groups)
