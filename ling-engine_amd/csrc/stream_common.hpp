@@ -4,6 +4,7 @@
 #pragma once
 
 #include "lq_common.hpp"
+#include "lq_div.hpp"
 #include "lq_workspace.hpp"
 
 #include <cstddef>
@@ -312,17 +313,6 @@ __device__ __forceinline__ void epilogue(const StreamArgs& a, int mi, int wtile0
 // Workgroup p's units are [unit_start(p), unit_start(p + 1)); wg_of_unit is the workgroup of unit u.
 __device__ __forceinline__ int wg_of_unit(int u, int P, int U) { return ((u + 1) * P - 1) / U; }
 __device__ __forceinline__ int unit_start(int p, int P, int U) { return p * U / P; }
-// floor(n / d) for n >= 0, d > 0, n + d < 2^31 and a quotient below 2^21, from rd = 1.f / d: the float
-// estimate n * rd is within 3 * 2^-24 relative of n / d, so within 0.4 of it, and its truncation is the quotient
-// or one off; one step each way corrects it. Eight instructions where an integer division takes about 35.
-__device__ __forceinline__ int div_by_rcp(int n, int d, float rd) {
-  int q = static_cast<int>(static_cast<float>(n) * rd);
-  if (q * d > n)
-    --q;
-  else if ((q + 1) * d <= n)
-    ++q;
-  return q;
-}
 
 // A segment's first tile group and workgroup, its workgroups P and its units U (see StreamArgs::wg0).
 struct SegSplit {
