@@ -127,6 +127,13 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
                                 const uint8_t* raw_scales, float scale2, const int* rows, const int* nrows, int cap,
                                 float* y, int K, int N, void* stream);
 
+/* Cache run-ahead: reads what a stream GEMM over (w, N, K) reads first, about `bytes` of it, and writes nothing, so
+ * that launch's first loads hit the caches after a latency-bound stretch. fp4: NVFP4 blob (coded: the scale-coded
+ * form), else FP8. w null or bytes 0: nothing happens. This library's split cuts K per workgroup, so the bytes
+ * taken are each workgroup's first units (tile group x chunk) of its own range, by the workgroup of the same index,
+ * not every tile's first chunks. src/core/kernels.cuh:405 l2_prefetch_weights (src/core/stream_gemm.cu:1864-1873) */
+int lq_l2_prefetch_weights(const uint8_t* w, int fp4, int coded, int N, int K, size_t bytes, void* stream);
+
 /* ---------------- rows path, BF16 formats (additive; per-channel FP8 scales, BF16 in and out) ---------------- */
 /* y[M][N] = bf16(wscale_n[n] * x . W^T), W tiled FP8, x BF16 [M][K]. Replaces the engine's linear_fp8
  * (reference src/core/engine.cpp:1272-1281) for per-channel checkpoints. */

@@ -92,6 +92,10 @@ inline void stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int 
   lq_check(lq_stream_gemm_gather_nvfp4(xh, xinv, M, w, raw_scales, scale2, rows, nrows, cap, y, K, N, s));
 }
 
+inline void l2_prefetch_weights(const uint8_t* w, bool fp4, bool coded, int N, int K, size_t bytes, hipStream_t s) {
+  lq_check(lq_l2_prefetch_weights(w, fp4 ? 1 : 0, coded ? 1 : 0, N, K, bytes, s));
+}
+
 // ---- rows path, BF16 formats (additive) ----
 inline void stream_fp8_pc(const uint16_t* x, int M, const uint8_t* w, const float* wscale_n, uint16_t* y, int N, int K,
                           hipStream_t s) {

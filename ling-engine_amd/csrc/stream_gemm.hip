@@ -842,6 +842,38 @@ __global__ void __launch_bounds__(kGatherThreads) __attribute__((amdgpu_waves_pe
   store(val);
 }
 
+// ---------------- cache run-ahead (reference l2_prefetch_tiles_kernel, src/core/stream_gemm.cu:822-840) ----------
+// Reads (and discards) what a stream GEMM over the same matrix reads first: for each of the launch's P workgroups,
+// the first nc units (tile group x chunk) of its stream-K range, block by block, one 4-byte load per 64-byte piece
+// so every cache line is fetched. Workgroup b takes the range the GEMM's workgroup b takes (the same XCD-aware
+// permutation), so on a part that deals workgroups to XCDs by index the lines land in the L2 that GEMM workgroup
+// reads through. Nothing is written; the GEMM that follows computes the same bits.
+__global__ void __launch_bounds__(256) prefetch_units_kernel(const uint8_t* __restrict__ w, int C, int P, int U,
+                                                             int tpg, int tiles, int blk, long long code_base,
+                                                             int nc) {
+  const int b = static_cast<int>(blockIdx.x);
+  const int p = (P & 7) == 0 ? (b & 7) * (P >> 3) + (b >> 3) : b;
+  const int u0 = unit_start(p, P, U), n = min(nc, unit_start(p + 1, P, U) - u0);
+  const int pieces = tpg * blk / 64;  // 64-byte pieces of one unit's blocks
+  uint32_t sink = 0;
+  for (int k = 0; k < n; ++k) {
+    const int u = u0 + k, tg = u / C, c = u - tg * C;
+    for (int i = static_cast<int>(threadIdx.x); i < pieces; i += 256) {
+      const int ti = i * 64 / blk, tile = tg * tpg + ti;
+      if (tile < tiles)
+        sink += *reinterpret_cast<const uint32_t*>(w + (static_cast<size_t>(tile) * C + c) * blk + (i * 64 - ti * blk));
+    }
+    // coded NVFP4: each tile's 96 code bytes of the chunk, in the blob's code region (two 64-byte pieces)
+    if (code_base >= 0 && static_cast<int>(threadIdx.x) < 2 * tpg) {
+      const int tile = tg * tpg + (static_cast<int>(threadIdx.x) >> 1);
+      if (tile < tiles)
+        sink += *reinterpret_cast<const uint32_t*>(w + code_base + (static_cast<size_t>(tile) * C + c) * kCodeBytesFp4 +
+                                                   (threadIdx.x & 1) * 64);
+    }
+  }
+  asm volatile("" ::"v"(sink));  // keeps the loads
+}
+
 // ---------------- activation copies (reference src/core/stream_gemm.cu:480-566) ----------------
 // Grid (M, S): every block finds the row's largest magnitude (a maximum is exact in any order, so all
 // blocks agree) and converts its slice of K: xh = f16_rn(x * 2^(15 - e)), xinv = 2^(e - 15).
@@ -1579,6 +1611,25 @@ int lq_stream_gemm_gather_nvfp4(const uint16_t* xh, const float* xinv, int M, co
   else
     hipLaunchKernelGGL((gather_kernel<1, false, true>), dim3(cap / 16, cdiv(M, 16)), blk, 0, s, a);
   return check_launch("stream_gemm_gather");
+}
+
+int lq_l2_prefetch_weights(const uint8_t* w, int fp4, int coded, int N, int K, size_t bytes, void* stream) {
+  if (!w || bytes == 0) return LQ_OK;  // as the reference: nothing asked, nothing done
+  if (N <= 0 || N % 16 != 0 || K <= 0 || K % kChunk != 0)
+    return fail(LQ_ERR_SHAPE, "l2_prefetch_weights: N % 16 and K % 128 must be 0");
+  const int fmt = fp4 ? (coded ? kFp4Coded : kFp4) : kFp8;
+  const int C = K / kChunk, tiles = N / 16;
+  int T, tg, P;
+  matrix_split(fmt, false, N, C, T, tg, P);
+  const int tpg = group_rows(T, false) / 16;
+  const int blk = fmt == kFp8 ? kTileBytesFp8 : fmt == kFp4 ? kTileBytesFp4 : kValueBytesFp4;
+  const long long per_round = static_cast<long long>(P) * tpg * (blk + (coded && fp4 ? kCodeBytesFp4 : 0));
+  const long long want = static_cast<long long>(bytes) / per_round;
+  const int nc = static_cast<int>(std::min<long long>(C, std::max<long long>(1, want)));
+  const long long code_base = fmt == kFp4Coded ? static_cast<long long>(tiles) * C * kValueBytesFp4 : -1;
+  hipLaunchKernelGGL(prefetch_units_kernel, dim3(P), dim3(256), 0, static_cast<hipStream_t>(stream), w, C, P,
+                     tg * C, tpg, tiles, blk, code_base, nc);
+  return check_launch("l2_prefetch_weights");
 }
 
 int lq_stream_ffn_deadline_status(int* hit) {

@@ -40,6 +40,7 @@ SIGNATURES = {
     "lq_stream_gemm_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _I, _I, _P]),
     "lq_stream_gemm_multi": (_I, [_I, _P, _P, _I, _P, _I, _I, _P]),
     "lq_stream_gemm_gather_nvfp4": (_I, [_P, _P, _I, _P, _P, _F, _P, _P, _I, _P, _I, _I, _P]),
+    "lq_l2_prefetch_weights": (_I, [_P, _I, _I, _I, _I, _SZ, _P]),
     "lq_stream_fp8_pc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_noalloc": (_I, [_P, _I, _P, _P, _P, _I, _I, _P]),
     "lq_stream_fp8_pc_silu_mul": (_I, [_P, _I, _P, _P, _P, _P, _P, _I, _I, _P]),
@@ -325,6 +326,12 @@ def stream_gemm_gather_nvfp4(xh, xinv, w, raw_scales, scale2: float, rows, nrows
                                            scale2, _ptr(_dev(rows, torch.int32)), _ptr(_dev(nrows, torch.int32)), cap,
                                            _ptr(y), K, N, _stream()))
     return y
+
+
+def l2_prefetch_weights(w, fp4: bool, coded: bool, N: int, K: int, nbytes: int):
+    """Warms the caches with about nbytes of what a stream GEMM over (w, N, K) reads first; writes nothing."""
+    _check(lib.lq_l2_prefetch_weights(_ptr(w), int(fp4), int(coded), N, K, int(nbytes),
+                                      _stream()))
 
 
 def stream_gemm_multi(nvfp4: bool, xh, xinv, targets, K: int):

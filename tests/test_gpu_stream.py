@@ -294,6 +294,38 @@ def test_coded_equals_raw_and_multi_equals_separate(L):
     assert np.array_equal(y1.cpu().numpy(), y8) and np.array_equal(y2.cpu().numpy(), y8)
 
 
+def test_l2_prefetch_weights_changes_nothing(L):
+    """The cache run-ahead (reference kernels.cuh:405 l2_prefetch_weights) writes nothing: every GEMM after it gives
+    the same bits, FP8 and NVFP4 raw and coded, at budgets from one unit per workgroup to the whole matrix; a null
+    blob or a zero budget is a no-op, as in the reference (stream_gemm.cu:1865); a bad shape is an error."""
+    N, K = 2048, 5120
+    q, s = fp8_weights(77, N, K)
+    tw, sd = L.retile_fp8(to_dev(q)), to_dev(s)
+    x = bf16_dev(O.normal_bf16(78, 1.0, (17, K)))
+    before = bf16_host(L.stream_fp8_pc(x, tw, sd, N))
+    for nbytes in (1, 1 << 20, 1 << 40):
+        L.l2_prefetch_weights(tw, False, False, N, K, nbytes)
+        assert np.array_equal(bf16_host(L.stream_fp8_pc(x, tw, sd, N)), before), f"fp8 nbytes={nbytes}"
+    v, sc, g, _ = O.quant_nvfp4(O.normal_bf16(79, 0.02, (N, K)))
+    ok, table, code_of = O.scale_code_table(sc)
+    assert ok
+    raw = L.retile_nvfp4(to_dev(v), to_dev(sc))
+    coded, _ = L.retile_nvfp4_coded(to_dev(v), to_dev(sc), to_dev(code_of))
+    for blob, tab in ((raw, None), (coded, to_dev(table))):
+        ref = bf16_host(L.stream_nvfp4_bf16(x, blob, tab, g, N))
+        for nbytes in (1, 1 << 22, 1 << 40):
+            L.l2_prefetch_weights(blob, True, tab is not None, N, K, nbytes)
+            got = bf16_host(L.stream_nvfp4_bf16(x, blob, tab, g, N))
+            assert np.array_equal(got, ref), f"nvfp4 coded={tab is not None} nbytes={nbytes}"
+    torch.cuda.synchronize()
+    L.l2_prefetch_weights(None, False, False, N, K, 1 << 20)
+    L.l2_prefetch_weights(tw, False, False, 17, K, 0)  # zero budget: not even the shape is looked at
+    with pytest.raises(L.LingGemmError):
+        L.l2_prefetch_weights(tw, False, False, 17, K, 1 << 20)
+    with pytest.raises(L.LingGemmError):
+        L.l2_prefetch_weights(tw, False, False, N, 100, 1 << 20)
+
+
 @pytest.mark.parametrize("N,K", [(4096, 2560), (8192, 5120)])
 def test_stream_gemm_gather_nvfp4_bit_exact(L, N, K):
     """The sparse head (reference tests/stream_tests.cu:271-300): a row subset, not in order, from the raw blob
