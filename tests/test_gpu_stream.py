@@ -342,8 +342,8 @@ def test_stream_gemm_gather_nvfp4_bit_exact(L, N, K):
     cnt = rows.size
     cap = (cnt + 96 + 31) // 32 * 32
     drows = to_dev(rows)
-    x = O.normal_f32(61, 1.0, (68, K))
-    for M in [1, 11, 17, 33, 65, 68]:
+    x = O.normal_f32(61, 1.0, (80, K))
+    for M in [1, 11, 17, 33, 65, 68, 80]:
         xh, xinv = L.to_half_rows(to_dev(x[:M]))
         full = L.stream_gemm_nvfp4(xh, xinv, raw, None, g, N, K).cpu().numpy()
         for c in [cnt, 5, 0]:
